@@ -1,0 +1,204 @@
+"""Benchmark: slot_murmurate forward+backward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu]
+
+A step is one forward+backward of the README-form slot_murmurate over one
+synthetic batch (seeded N(0,1) draws), inputs resident
+in HBM.  `value` is tokens/s over exactly K timed steps (HIP-synchronised on
+both sides).  A second pass over the same K steps records HIP events around
+every kernel launch (on the stream the kernels run on) for the per-kernel
+durations behind the roofline fraction.  The CPU baseline times the CPU oracle
+(a PyTorch restatement of the reference's reference.py) on the host cores.
+Prints one JSON line.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "murmurative-attention_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "tokens/sec fwd+bwd slot_murmurate H=16 N=8192 d=64 bf16; % of roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+CONFIGS = {
+    # name: (B, H, N, D, M, rounds, causal, dtype, slots_k std, slots_v std)
+    "2": (4, 8, 2048, 64, 256, 3, False, "float16", 1.0, 0.02),
+    "3": (1, 16, 8192, 64, 256, 3, False, "bfloat16", 1.0, 0.02),
+    "4": (1, 16, 65536, 128, 256, 3, True, "bfloat16", 1.0, 0.02),
+}
+
+
+def byte_model(B, H, N, D, M, R, e):
+    """Algorithmic HBM bytes per launch of each kernel class (README form).
+
+    Every tensor is counted once per launch: tokens q / grad_out / out (T*D*e),
+    u16 index rows (T*16), float32 weights and softmax grads (T*28), float32
+    slot tables [B*H,M,D] (S), weight sums (B*H*M*4)."""
+    T = B * H * N
+    tok = T * D * e
+    S = B * H * M * D * 4
+    idx, w = T * 16, T * 28
+    Wb = B * H * M * 4
+    per_launch = {
+        # q + slot keys in; u16 indices and weights out (+ int64 indices in the last round)
+        "select_attend": (R * (tok + S + idx + w) + T * 56) / R,
+        # q, R rounds of (indices, weights, value table) in; out written
+        "gather_out": tok + R * (idx + w + S) + tok,
+        # q, indices, weights, 2 old slot tables in; 2 new tables, key sums, weight sums out
+        "seg_update": tok + idx + w + 2 * S + 2 * S + S + Wb,
+        # q, grad_out, ds, weights, indices, 2 carries in; 2 slot grads out
+        "seg_attbwd": 2 * tok + w + w + idx + 2 * S + 2 * S,
+        # 2 grads, key sums, weight sums in; dK, 2 carries, dW out
+        "du": 2 * S + S + Wb + 3 * S + Wb,
+        # grad_out, q, indices, weights, value table, dK, dW in; ds out (external grad_w once)
+        "tok_bwd": 2 * tok + idx + w + 2 * S + Wb + w,
+        # grad_out in; R rounds of (indices, weights, ds, key table, dK) in; dq out
+        "tok_grad": tok + R * (idx + 2 * w + 2 * S) + tok,
+        # input slots in (2 tables, 16-bit) + fp32 states out, and fp32 grads -> 16-bit slot grads
+        "conversions": 2 * (B * H * M * D * e) + 2 * S,
+    }
+    flops = {"select_attend": 2.0 * T * M * D}
+    return per_launch, flops
+
+
+def make_inputs(cfg, device, seed=42):
+    import torch
+    B, H, N, D, M, R, causal, dt, sk_std, sv_std = cfg
+    dtype = getattr(torch, dt)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, N, D, generator=g)
+    sk = torch.randn(B, H, M, D, generator=g) * sk_std
+    sv = torch.randn(B, H, M, D, generator=g) * sv_std
+    go = torch.randn(B, H, N, D, generator=g)
+    return [t.to(dtype).to(device) for t in (q, sk, sv, go)]
+
+
+def cpu_baseline(cfg, budget_s=20.0):
+    """Time the CPU oracle's forward+backward (autograd) on a bounded head sample."""
+    import torch
+    from oracle import murm_oracle as O
+    B, H, N, D, M, R, causal, dt, _, _ = cfg
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    q, sk, sv, go = make_inputs(cfg, "cpu", seed=42)
+
+    def run(h):
+        qq, kk, vv = (t[:, :h].detach().clone().requires_grad_(True) for t in (q, sk, sv))
+        t0 = time.perf_counter()
+        out, _, _ = O.murmurate_readme(qq, kk, vv, rounds=R, causal=causal)
+        torch.autograd.grad(out, (qq, kk, vv), go[:, :h])
+        return time.perf_counter() - t0
+
+    run(1)  # warm-up
+    t1 = run(1)
+    heads = max(1, min(H, int(budget_s / 3.0 / max(t1, 1e-3))))
+    times = sorted(run(heads) for _ in range(3))
+    med = times[1]
+    # heads are independent: the full call costs H/heads times the sample
+    tok_s = B * N * heads / (H * med)
+    return {"value": round(tok_s, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle/murm_oracle.py murmurate_readme fwd+bwd (autograd), {dt} inputs, "
+                       f"B={B}, {heads} of {H} heads, N={N}, d={D}, M={M}, R={R}; median of 3 after "
+                       f"1 warm-up, {med:.3f} s; tokens/s = B*N*(heads/H) / time")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {a.gpus}); the kernels run per (b,h) "
+              f"with no cross-GPU work in this build.", file=sys.stderr)
+        return 2
+
+    import torch
+    import murmurative
+    from murmurative import capi
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[a.config]
+    B, H, N, D, M, R, causal, dt, _, _ = cfg
+    q, sk, sv, go = make_inputs(cfg, dev)
+    for t in (q, sk, sv):
+        t.requires_grad_(True)
+
+    def step():
+        out, idx, w = murmurative.slot_murmurate(q, sk, sv, rounds=R, causal=causal)
+        return torch.autograd.grad(out, (q, sk, sv), go)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = 1e3 * elapsed / a.steps
+    value = B * N * a.steps / elapsed
+
+    # second pass: HIP events around every launch, same K steps
+    capi.timing_reset()
+    capi.timing_enable(True)
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    capi.timing_enable(False)
+    kt = capi.timing_read()
+    capi.timing_reset()
+
+    e = 2 if dt in ("bfloat16", "float16") else 4
+    per_launch, flops = byte_model(B, H, N, D, M, R, e)
+    kernels = {}
+    for name, (ms, n) in kt.items():
+        avg_us = 1e3 * ms / n
+        gbs = per_launch.get(name, 0.0) / (avg_us * 1e-6) / 1e9
+        kernels[name] = {"launches_per_step": n / a.steps, "avg_us": round(avg_us, 2),
+                         "ms_per_step": round(ms / a.steps, 4), "GB_s": round(gbs, 1),
+                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    dom = max(kt, key=lambda k: kt[k][0])
+    dk = kernels[dom]
+    roofline = {"kernel": dom, "bound": "hbm", "achieved": dk["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dk["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "bytes_per_launch": int(per_launch[dom]), "avg_us": dk["avg_us"]}
+    if "select_attend" in kt:
+        sa_ms, sa_n = kt["select_attend"]
+        tf = flops["select_attend"] / (sa_ms / sa_n * 1e-3) / 1e12
+        kernels["select_attend"]["score_gemm_TFLOPs"] = round(tf, 2)
+        kernels["select_attend"]["mfma_frac"] = round(tf / MFMA_BF16_PEAK_TFLOPS, 4)
+    device_ms = sum(ms for ms, _ in kt.values()) / a.steps
+
+    res = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": {"bfloat16": "bf16", "float16": "fp16", "float32": "fp32"}[dt],
+        "data": "synthetic: seeded N(0,1) draws shaped as BASELINE.json configs (slots_v ~ N(0,0.02))",
+        "config": {"workload": f"slot_murmurate README form fwd+bwd, BASELINE configs[{int(a.config) - 1}]",
+                   "B": B, "H": H, "N": N, "head_dim": D, "M": M, "top_k": 7, "rounds": R, "causal": causal,
+                   "tokens_per_step": B * N},
+        "roofline": roofline,
+        "kernels": kernels,
+        "device_ms_per_step_in_kernels": round(device_ms, 4),
+    }
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(cfg, a.cpu_budget)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,177 @@
+// Shared device helpers for the gfx950 slot_murmurate kernels.
+//
+// Layout conventions used by every kernel in this directory:
+//   * Token tensors (q, x, k/v projections, grad_out, grad_q) are addressed as
+//     base + b*sb + h*sh + n*sn + d (element strides, d contiguous), so the
+//     [B,H,N,D] README layout and the [B,N,H,Dh] legacy views both work
+//     without a copy.
+//   * Slot state between rounds is float32, contiguous [B*H, M, D].
+//   * Per-round indices are uint16 rows of 8 (7 used, the 8th is IDX_NONE),
+//     contiguous [B*H, N, 8]; weights are float32 [B*H, N, 7].
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace murm {
+
+constexpr int KN = 7;                 // slots per token (reference.py:38, k=7)
+constexpr int IDX_ROW = 8;            // padded index row (u16)
+constexpr uint16_t IDX_NONE = 0xFFFF; // never matches a slot
+constexpr int MAX_ROUNDS = 16;
+
+enum DType : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- scalars ---
+
+template <typename T> __device__ __forceinline__ float to_f(T v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f(float v) { return (T)v; }
+
+// 8 consecutive elements of a token row, converted to float; elements at
+// d >= D read as zero.  `vec` says the row start is 16-byte aligned and the
+// full 8 elements are in range, so one wide load can be used.
+template <typename T>
+__device__ __forceinline__ void load8(const T* __restrict__ row, int d0, int D, bool vec, float (&o)[8]) {
+  if (vec && d0 + 8 <= D) {
+    if constexpr (sizeof(T) == 2) {
+      uint4 raw = *reinterpret_cast<const uint4*>(row + d0);
+      const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = to_f(e[i]);
+    } else {
+      float4 a = *reinterpret_cast<const float4*>(row + d0);
+      float4 b = *reinterpret_cast<const float4*>(row + d0 + 4);
+      o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+      o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (d0 + i < D) ? to_f(row[d0 + i]) : 0.f;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* __restrict__ row, int d0, int D, bool vec, const float (&v)[8]) {
+  if (vec && d0 + 8 <= D) {
+    if constexpr (sizeof(T) == 2) {
+      uint4 raw;
+      T* e = reinterpret_cast<T*>(&raw);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = from_f<T>(v[i]);
+      *reinterpret_cast<uint4*>(row + d0) = raw;
+    } else {
+      *reinterpret_cast<float4*>(row + d0) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(row + d0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (d0 + i < D) row[d0 + i] = from_f<T>(v[i]);
+  }
+}
+
+// 8 floats from fp32 slot state (rows are D floats; D % 4 == 0 for the vector path)
+__device__ __forceinline__ void load8f(const float* __restrict__ row, int d0, int D, float (&o)[8]) {
+  if (d0 + 8 <= D && (D & 3) == 0) {
+    float4 a = *reinterpret_cast<const float4*>(row + d0);
+    float4 b = *reinterpret_cast<const float4*>(row + d0 + 4);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (d0 + i < D) ? row[d0 + i] : 0.f;
+  }
+}
+
+// ------------------------------------------------------------ wave ops ---
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// ---------------------------------------------------- packed top-k keys ---
+// A selection key is the float score with its low `bits` mantissa bits
+// replaced by the slot index.  Float max/med3 then carry the index with the
+// score, so inserting one score into a sorted top-7 list is 1 max + 6 med3.
+// Truncation costs 2^-(23-bits) relative precision, far below the 1e-3
+// relative gap at which an index is considered decided.  Masked scores use
+// -FLT_MAX (finite, so the index bits survive); padding uses -inf, which can
+// never be selected while M >= 7.
+
+__device__ __forceinline__ float make_key(float s, uint32_t hi_mask, uint32_t m) {
+  return __uint_as_float((__float_as_uint(s) & hi_mask) | m);
+}
+__device__ __forceinline__ uint32_t key_slot(float k, uint32_t lo_mask) {
+  return __float_as_uint(k) & lo_mask;
+}
+__device__ __forceinline__ float key_score(float k, uint32_t hi_mask) {
+  return __uint_as_float(__float_as_uint(k) & hi_mask);
+}
+constexpr float MASKED_SCORE = -3.4028234663852886e38f;  // -FLT_MAX
+__device__ __forceinline__ bool key_masked(float k) { return k <= -1.0e38f; }
+
+template <int K>
+__device__ __forceinline__ void topk_insert(float (&a)[K], float x) {
+  float b[K];
+  b[0] = fmaxf(a[0], x);
+#pragma unroll
+  for (int j = 1; j < K; ++j) b[j] = __builtin_amdgcn_fmed3f(a[j - 1], a[j], x);
+#pragma unroll
+  for (int j = 0; j < K; ++j) a[j] = b[j];
+}
+
+// ------------------------------------------------------------------ MFMA ---
+
+__device__ __forceinline__ f32x4 mfma_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Operand element type of the 16-bit MFMA for a token dtype.
+template <typename T> struct Mfma16;
+template <> struct Mfma16<__bf16> { using elem = __bf16; using vec = bf16x8; };
+template <> struct Mfma16<_Float16> { using elem = _Float16; using vec = f16x8; };
+
+// -------------------------------------------------------------- strides ---
+
+struct TokView {      // a [B,H,N,D] view of a token tensor
+  const void* p;
+  int64_t sb, sh, sn;  // element strides
+  int vec;             // 16-byte aligned rows (wide loads allowed)
+};
+struct TokViewMut {
+  void* p;
+  int64_t sb, sh, sn;
+  int vec;
+};
+
+template <typename T>
+__device__ __forceinline__ const T* tok_row(const TokView& v, int b, int h, int64_t n) {
+  return reinterpret_cast<const T*>(v.p) + b * v.sb + h * v.sh + n * v.sn;
+}
+template <typename T>
+__device__ __forceinline__ T* tok_row_mut(const TokViewMut& v, int b, int h, int64_t n) {
+  return reinterpret_cast<T*>(v.p) + b * v.sb + h * v.sh + n * v.sn;
+}
+
+// Per-round pointer tables for the kernels that sum over every round.
+struct RoundPtrs {
+  const uint16_t* idx[MAX_ROUNDS];   // [BH, N, 8]
+  const float* w[MAX_ROUNDS];        // [BH, N, 7]
+  const float* a[MAX_ROUNDS];        // slot rows gathered with weight w (fp32 [BH, M, D])
+  const float* b[MAX_ROUNDS];        // second gathered table (optional)
+  const float* c[MAX_ROUNDS];        // per-(token, j) coefficient for table b (optional)
+};
+
+}  // namespace murm

@@ -1,0 +1,120 @@
+// Kernel parameter blocks and launchers (internal to libmurmurative_hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "murm_common.h"
+
+namespace murm {
+
+struct SAParams {
+  TokView q;
+  const float* sk;        // fp32 slot keys [BH, M, D]
+  int B, H, N, D, M, em;
+  int causal;
+  float scale;
+  uint32_t hi_mask, lo_mask;  // packed-key split (low bits carry the slot)
+  const uint8_t* mask;        // optional, nonzero = keep; element strides over (b,h,n,m)
+  int64_t mk_sb, mk_sh, mk_sn, mk_sm;
+  const float* bias;          // optional position bias added to the unscaled score
+  int64_t bs_sb, bs_sh, bs_sn, bs_sm;
+  uint16_t* idx16;            // [BH, N, 8] or null
+  int64_t* idx64;             // [BH, N, 7] or null
+  float* w;                   // [BH, N, 7]
+};
+
+struct OutParams {
+  TokView base;     // optional residual (p == null -> 0)
+  TokViewMut out;
+  int B, H, N, D, M, R;
+  RoundPtrs rp;     // idx[r], w[r], a[r] = value table of round r
+};
+
+enum SegMode : int { SEG_UPDATE = 0, SEG_ATTBWD = 1 };
+
+struct SegParams {
+  int B, H, N, D, M, K;
+  const uint16_t* idx;   // [BH, N, 8]
+  const float* wgt;      // [BH, N, K] weights
+  const float* ds;       // [BH, N, K] softmax-backward (ATTBWD)
+  float ds_scale;        // c = attend scale (ATTBWD)
+  TokView va;            // UPDATE: token keys; ATTBWD: queries
+  TokView vb;            // UPDATE: token values; ATTBWD: grad of the attend output
+  int b_same_as_a;       // UPDATE: token values are the token keys
+  // UPDATE
+  const float* sk_old; const float* sv_old;  // fp32 [BH, M, D]
+  float* sk_new; float* sv_new;              // fp32 [BH, M, D] (null: sums only)
+  float* ksum; float* vsum; float* wsum;     // optional saved sums
+  float alpha, gamma, eps;
+  int diffuse;
+  // ATTBWD
+  const float* carry_k; const float* carry_v;  // optional pass-through grads
+  float* gk_out; float* gv_out;                // fp32 [BH, M, D]
+};
+
+struct DuParams {
+  int B, H, M, D;
+  const float* Gk; const float* Gv;   // grads w.r.t. the post-diffusion slots
+  const float* K; const float* V; const float* W;  // forward sums of the round
+  float alpha, gamma, eps;
+  int transpose;     // apply the diffusion adjoint first
+  int combine_dk;    // token keys == token values: write dKk + dKv to dk_out
+  float* dk_out; float* dv_out; float* dW_out;
+  float* carry_k; float* carry_v;
+};
+
+struct TokBwdParams {
+  int B, H, N, D, M;
+  TokView g, tk, tv;
+  const uint16_t* idx; const float* w;
+  const float* sv;              // g.sv term (null: absent)
+  const float* dkk; const float* dkv;  // tk.dKk / tv.dKv terms (null: absent)
+  const float* dW;              // [BH, M] (null: absent)
+  const float* gw;              // [BH, N, 7] external weight grads (null: absent)
+  float* ds_out;                // softmax backward (null: skip)
+  float* dw_out;                // raw dw (null: skip)
+};
+
+struct TokGradParams {
+  int B, H, N, D, M, R;
+  float c;
+  TokView g;                    // residual term added to dq (p == null: none)
+  TokViewMut dq, dtk, dtv;      // outputs (p == null: skip)
+  int shared_kv;                // w.dK terms go to dq (README form)
+  const uint16_t* idx[MAX_ROUNDS];
+  const float* w[MAX_ROUNDS];
+  const float* ds[MAX_ROUNDS];
+  const float* sk[MAX_ROUNDS];
+  const float* dkk[MAX_ROUNDS];
+  const float* dkv[MAX_ROUNDS];
+};
+
+struct AttendIdxParams {
+  int B, H, N, D, M;
+  TokView q;
+  const float* sk;        // fp32 [BH, M, D]
+  const uint16_t* idx;    // [BH, N, 8]
+  float scale;
+  float* w;               // [BH, N, 7]
+};
+
+size_t sa_lds_bytes(int dtype, int DP, int M);
+hipError_t launch_attend_idx(int dtype, int DP, const AttendIdxParams& p, hipStream_t st);
+hipError_t launch_select_attend(int dtype, int DP, const SAParams& p, hipStream_t st);
+hipError_t launch_gather_out(int dtype, int DP, const OutParams& p, hipStream_t st);
+hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, hipStream_t st);
+hipError_t launch_du(const DuParams& p, hipStream_t st);
+hipError_t launch_tok_bwd(int dtype, int DP, const TokBwdParams& p, hipStream_t st);
+hipError_t launch_tok_grad(int dtype, int DP, const TokGradParams& p, hipStream_t st);
+hipError_t launch_to_state(int dtype, const void* src, int64_t sb, int64_t sh, int64_t sm, float* dst,
+                           int B, int H, int M, int D, hipStream_t st);
+hipError_t launch_from_state(int dtype, const float* src, void* dst, int64_t sb, int64_t sh, int64_t sm,
+                             int B, int H, int M, int D, hipStream_t st);
+hipError_t launch_idx_pack(const int64_t* src, uint16_t* dst, int64_t rows, int K, int M, hipStream_t st);
+hipError_t launch_stencil(int dtype, void* x, int64_t sb, int64_t sh, int64_t sm, void* out, int64_t ob,
+                          int64_t oh, int64_t om, int B, int H, int M, int D, float g, int adjoint,
+                          hipStream_t st);
+
+}  // namespace murm

@@ -1,0 +1,451 @@
+// Select + attend (one round) and the per-token output gather.
+//
+// select_attend: for every token, scores s_m = q . sk_m over all M slots on
+// MFMA (the N x M score matrix never leaves registers), top-7 by a packed
+// float key (score with the slot index in its low mantissa bits), then the
+// softmax over the 7 selected scores.  Writes indices (u16 rows and/or the
+// int64 API tensor) and float32 weights.  Semantics: reference.py:6-68.
+//
+// Slot keys come from float32 state.  The 16-bit MFMA path splits each key
+// into hi + lo halves of the token dtype (hi = rn(x), lo = rn(x - hi)) and
+// accumulates q.lo + q.hi in float32, which reproduces the float32 score to
+// ~2^-16 relative: selection is decided to far better than the 1e-3 relative
+// gap used by the parity gate.  float32 tokens use the f32 MFMA and recompute
+// the seven winning scores exactly before the softmax.
+//
+// MFMA 16x16x32 lane layout (gfx950): A row = lane&15, k = 8*(lane>>4)+i;
+// B col = lane&15, same k; D holds rows 4*(lane>>4)+r of column lane&15.
+// Here A = slot keys (rows = slots), B = tokens (cols), so every lane holds
+// four consecutive slot scores of one token per 16-slot tile.
+
+#include "murm_common.h"
+#include "murm_launch.h"
+
+namespace murm {
+
+namespace {
+
+template <int DP> struct SAShape {
+  static constexpr int G = (DP <= 64) ? 4 : 2;   // 16-token groups per wave
+  static constexpr int WAVES = 4;
+  static constexpr int TOK = WAVES * G * 16;     // tokens per block
+};
+
+// mask / bias / causal / effective_M slow path for one score
+__device__ __forceinline__ float masked_key(const SAParams& p, int b, int h, int n, int m,
+                                            float s) {
+  if (m >= p.M) return -INFINITY;
+  bool dead = (m >= p.em) || (p.causal && m > n) || (n >= p.N);
+  if (!dead && p.mask)
+    dead = p.mask[b * p.mk_sb + h * p.mk_sh + (int64_t)n * p.mk_sn + m * p.mk_sm] == 0;
+  if (!dead && p.bias)
+    s += p.bias[b * p.bs_sb + h * p.bs_sh + (int64_t)n * p.bs_sn + m * p.bs_sm];
+  return make_key(dead ? MASKED_SCORE : s, p.hi_mask, (uint32_t)m);
+}
+
+// Merge the four per-lane lists of a token (lanes l, l^16, l^32, l^48).
+template <int G>
+__device__ __forceinline__ void merge_quads(float (&tk)[G][KN]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int x = 16; x <= 32; x <<= 1) {
+      float o[KN];
+#pragma unroll
+      for (int j = 0; j < KN; ++j) o[j] = shfl_xor_f(tk[g][j], x);
+#pragma unroll
+      for (int j = 0; j < KN; ++j) topk_insert(tk[g], o[j]);
+    }
+  }
+}
+
+__device__ __forceinline__ void softmax7(const float (&sc)[KN], float scale, float (&w)[KN]) {
+  float z[KN], zmax = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < KN; ++j) { z[j] = scale * sc[j]; zmax = fmaxf(zmax, z[j]); }
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < KN; ++j) { z[j] = __expf(z[j] - zmax); sum += z[j]; }
+  const float inv = 1.0f / sum;
+#pragma unroll
+  for (int j = 0; j < KN; ++j) w[j] = z[j] * inv;
+}
+
+__device__ __forceinline__ void write_token(const SAParams& p, int bh, int n, const uint32_t (&slot)[KN],
+                                            const float (&w)[KN]) {
+  const int64_t row = (int64_t)bh * p.N + n;
+  if (p.idx16) {
+    uint4 r;
+    r.x = slot[0] | (slot[1] << 16);
+    r.y = slot[2] | (slot[3] << 16);
+    r.z = slot[4] | (slot[5] << 16);
+    r.w = slot[6] | ((uint32_t)IDX_NONE << 16);
+    *reinterpret_cast<uint4*>(p.idx16 + row * IDX_ROW) = r;
+  }
+  if (p.idx64) {
+#pragma unroll
+    for (int j = 0; j < KN; ++j) p.idx64[row * KN + j] = (int64_t)slot[j];
+  }
+#pragma unroll
+  for (int j = 0; j < KN; ++j) p.w[row * KN + j] = w[j];
+}
+
+// Raw 8-element load of a 16-bit token row into an MFMA operand (zero fill).
+template <typename T, typename V>
+__device__ __forceinline__ V load_operand8(const T* row, int d0, int D, bool vec) {
+  V v;
+  if (vec && d0 + 8 <= D) {
+    uint4 raw = *reinterpret_cast<const uint4*>(row + d0);
+    v = *reinterpret_cast<V*>(&raw);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (d0 + i < D) ? row[d0 + i] : (T)0.f;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit tokens (bf16 / fp16): hi/lo split keys in LDS, 16x16x32 MFMA
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void sa_kernel16(SAParams p) {
+  using V = typename Mfma16<T>::vec;
+  constexpr int G = SAShape<DP>::G;
+  constexpr int KC = DP / 32;
+  constexpr int ROW = DP + 8;  // LDS row stride in elements (16 B pad)
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* lhi = reinterpret_cast<T*>(smem);
+  const int Mp = (p.M + 15) & ~15;
+  T* llo = lhi + Mp * ROW;
+
+  const int bh = blockIdx.y;
+  const int b = bh / p.H, h = bh % p.H;
+  const float* skb = p.sk + (int64_t)bh * p.M * p.D;
+
+  for (int i = threadIdx.x; i < Mp * (DP / 4); i += blockDim.x) {
+    const int m = i / (DP / 4), d4 = (i % (DP / 4)) * 4;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (m < p.M && d4 + e < p.D) ? skb[(int64_t)m * p.D + d4 + e] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const T hi = (T)v[e];
+      const T lo = (T)(v[e] - (float)hi);
+      lhi[m * ROW + d4 + e] = hi;
+      llo[m * ROW + d4 + e] = lo;
+    }
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int quad = lane >> 4, col = lane & 15;
+  const int tok0 = blockIdx.x * SAShape<DP>::TOK + wave * (G * 16);
+  if (tok0 >= p.N) return;  // whole wave past the end (no block-wide sync below)
+
+  V bq[G][KC];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int n = tok0 + 16 * g + col;
+    const T* row = tok_row<T>(p.q, b, h, n < p.N ? n : 0);
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      bq[g][kc] = load_operand8<T, V>(row, 32 * kc + 8 * quad, p.D, p.q.vec);
+      if (n >= p.N) bq[g][kc] = V{};
+    }
+  }
+
+  float tk[G][KN];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < KN; ++j) tk[g][j] = -INFINITY;
+
+  const bool plain = !p.mask && !p.bias;
+  const int nT = Mp / 16;
+  for (int t = 0; t < nT; ++t) {
+    V ahi[KC], alo[KC];
+    const int arow = 16 * t + col;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      ahi[kc] = *reinterpret_cast<const V*>(lhi + arow * ROW + 32 * kc + 8 * quad);
+      alo[kc] = *reinterpret_cast<const V*>(llo + arow * ROW + 32 * kc + 8 * quad);
+    }
+    const int m0 = 16 * t + 4 * quad;
+    const bool tile_ok = plain && (16 * t + 16 <= p.em);
+    f32x4 acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[g] = mfma_16x16x32(alo[kc], bq[g][kc], acc[g]);
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[g] = mfma_16x16x32(ahi[kc], bq[g][kc], acc[g]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int gmin = tok0 + 16 * g;
+      const bool fast = tile_ok && (!p.causal || 16 * t + 15 <= gmin) && (gmin + 16 <= p.N);
+      if (fast) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
+      } else {
+        const int n = gmin + col;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) topk_insert(tk[g], masked_key(p, b, h, n, m0 + r, acc[g][r]));
+      }
+    }
+  }
+
+  merge_quads<G>(tk);
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int n = tok0 + 16 * g + col;
+    uint32_t slot[KN];
+    float sc[KN];
+    bool masked = false;
+#pragma unroll
+    for (int j = 0; j < KN; ++j) {
+      slot[j] = key_slot(tk[g][j], p.lo_mask);
+      sc[j] = key_score(tk[g][j], p.hi_mask);
+      masked |= key_masked(tk[g][j]);
+    }
+    // A selected slot whose selection score was masked (causal prefix,
+    // effective_M < 7, masked token) still attends with its real q.sk
+    // (reference.py:56-63): recompute those scores from the LDS keys.
+    if (__any(masked)) {
+      float part[KN];
+#pragma unroll
+      for (int j = 0; j < KN; ++j) {
+        part[j] = 0.f;
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+          const int d0 = 32 * kc + 8 * quad;
+          const V hv = *reinterpret_cast<const V*>(lhi + slot[j] * ROW + d0);
+          const V lv = *reinterpret_cast<const V*>(llo + slot[j] * ROW + d0);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) part[j] += (float)bq[g][kc][i] * ((float)hv[i] + (float)lv[i]);
+        }
+        part[j] += shfl_xor_f(part[j], 16);
+        part[j] += shfl_xor_f(part[j], 32);
+      }
+      if (masked)
+#pragma unroll
+        for (int j = 0; j < KN; ++j) sc[j] = part[j];
+    }
+    float w[KN];
+    softmax7(sc, p.scale, w);
+    if (quad == 0 && n < p.N) write_token(p, bh, n, slot, w);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// float32 tokens: f32 keys in LDS, 16x16x4 f32 MFMA, exact softmax scores
+// ---------------------------------------------------------------------------
+template <int DP>
+__global__ __launch_bounds__(256) void sa_kernel32(SAParams p) {
+  constexpr int G = SAShape<DP>::G;
+  constexpr int KK = DP / 4;
+  constexpr int ROW = DP + 4;
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* lsk = reinterpret_cast<float*>(smem);
+  const int Mp = (p.M + 15) & ~15;
+
+  const int bh = blockIdx.y;
+  const int b = bh / p.H, h = bh % p.H;
+  const float* skb = p.sk + (int64_t)bh * p.M * p.D;
+  for (int i = threadIdx.x; i < Mp * DP; i += blockDim.x) {
+    const int m = i / DP, d = i % DP;
+    lsk[m * ROW + d] = (m < p.M && d < p.D) ? skb[(int64_t)m * p.D + d] : 0.f;
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int quad = lane >> 4, col = lane & 15;
+  const int tok0 = blockIdx.x * SAShape<DP>::TOK + wave * (G * 16);
+  if (tok0 >= p.N) return;
+
+  float bq[G][KK];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int n = tok0 + 16 * g + col;
+    const float* row = tok_row<float>(p.q, b, h, n < p.N ? n : 0);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const int d = 4 * kk + quad;
+      bq[g][kk] = (n < p.N && d < p.D) ? row[d] : 0.f;
+    }
+  }
+  float tk[G][KN];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < KN; ++j) tk[g][j] = -INFINITY;
+
+  const bool plain = !p.mask && !p.bias;
+  const int nT = Mp / 16;
+  for (int t = 0; t < nT; ++t) {
+    const float* arow = lsk + (16 * t + col) * ROW + quad;
+    f32x4 acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const float a = arow[4 * kk];
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[g] = mfma_16x16x4(a, bq[g][kk], acc[g]);
+    }
+    const int m0 = 16 * t + 4 * quad;
+    const bool tile_ok = plain && (16 * t + 16 <= p.em);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int gmin = tok0 + 16 * g;
+      const bool fast = tile_ok && (!p.causal || 16 * t + 15 <= gmin) && (gmin + 16 <= p.N);
+      if (fast) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
+      } else {
+        const int n = gmin + col;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) topk_insert(tk[g], masked_key(p, b, h, n, m0 + r, acc[g][r]));
+      }
+    }
+  }
+
+  merge_quads<G>(tk);
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int n = tok0 + 16 * g + col;
+    uint32_t slot[KN];
+    float sc[KN];
+#pragma unroll
+    for (int j = 0; j < KN; ++j) {
+      slot[j] = key_slot(tk[g][j], p.lo_mask);
+      const float* srow = lsk + slot[j] * ROW + quad;
+      float part = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) part += bq[g][kk] * srow[4 * kk];
+      part += shfl_xor_f(part, 16);
+      part += shfl_xor_f(part, 32);
+      sc[j] = part;
+    }
+    float w[KN];
+    softmax7(sc, p.scale, w);
+    if (quad == 0 && n < p.N) write_token(p, bh, n, slot, w);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// out[n] = base[n] + sum_r sum_j w_rj * table_r[idx_rj]   (8 dims per thread)
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void gather_out_kernel(OutParams p) {
+  constexpr int DCH = DP / 8;
+  constexpr int TPB = 256 / DCH;  // tokens per block
+  const int bh = blockIdx.y;
+  const int b = bh / p.H, h = bh % p.H;
+  const int n = blockIdx.x * TPB + threadIdx.x / DCH;
+  const int dc = threadIdx.x % DCH;
+  if (n >= p.N) return;
+  const int d0 = dc * 8;
+  float acc[8];
+  if (p.base.p) {
+    load8<T>(tok_row<T>(p.base, b, h, n), d0, p.D, p.base.vec, acc);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  }
+  const int64_t row = (int64_t)bh * p.N + n;
+  for (int r = 0; r < p.R; ++r) {
+    const uint4 ir = *reinterpret_cast<const uint4*>(p.rp.idx[r] + row * IDX_ROW);
+    const uint32_t sl[KN] = {ir.x & 0xFFFF, ir.x >> 16, ir.y & 0xFFFF, ir.y >> 16,
+                             ir.z & 0xFFFF, ir.z >> 16, ir.w & 0xFFFF};
+    const float* wr = p.rp.w[r] + row * KN;
+    const float* tab = p.rp.a[r] + (int64_t)bh * p.M * p.D;
+#pragma unroll
+    for (int j = 0; j < KN; ++j) {
+      const float wj = wr[j];
+      float v[8];
+      load8f(tab + (int64_t)sl[j] * p.D, d0, p.D, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += wj * v[i];
+    }
+  }
+  store8<T>(tok_row_mut<T>(p.out, b, h, n), d0, p.D, p.out.vec, acc);
+}
+
+template <typename T, int DP>
+hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
+  const int Mp = (p.M + 15) & ~15;
+  dim3 grid((p.N + SAShape<DP>::TOK - 1) / SAShape<DP>::TOK, p.B * p.H);
+  if constexpr (sizeof(T) == 2) {
+    const size_t lds = 2 * (size_t)Mp * (DP + 8) * sizeof(T);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sa_kernel16<T, DP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((sa_kernel16<T, DP>), grid, dim3(256), lds, st, p);
+  } else {
+    const size_t lds = (size_t)Mp * (DP + 4) * sizeof(float);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sa_kernel32<DP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((sa_kernel32<DP>), grid, dim3(256), lds, st, p);
+  }
+  return hipGetLastError();
+}
+
+template <typename T, int DP>
+hipError_t launch_out_t(const OutParams& p, hipStream_t st) {
+  constexpr int TPB = 256 / (DP / 8);
+  dim3 grid((p.N + TPB - 1) / TPB, p.B * p.H);
+  hipLaunchKernelGGL((gather_out_kernel<T, DP>), grid, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t sa_lds_bytes(int dtype, int DP, int M) {
+  const size_t Mp = (size_t)((M + 15) & ~15);
+  return dtype == DT_F32 ? Mp * (DP + 4) * 4 : 2 * Mp * (DP + 8) * 2;
+}
+
+hipError_t launch_select_attend(int dtype, int DP, const SAParams& p, hipStream_t st) {
+#define MURM_SA(T)                                            \
+  switch (DP) {                                               \
+    case 32: return launch_sa_t<T, 32>(p, st);                \
+    case 64: return launch_sa_t<T, 64>(p, st);                \
+    case 128: return launch_sa_t<T, 128>(p, st);              \
+    default: return hipErrorInvalidValue;                     \
+  }
+  switch (dtype) {
+    case DT_BF16: MURM_SA(__bf16)
+    case DT_F16: MURM_SA(_Float16)
+    case DT_F32: MURM_SA(float)
+    default: return hipErrorInvalidValue;
+  }
+#undef MURM_SA
+}
+
+hipError_t launch_gather_out(int dtype, int DP, const OutParams& p, hipStream_t st) {
+#define MURM_OUT(T)                                           \
+  switch (DP) {                                               \
+    case 32: return launch_out_t<T, 32>(p, st);               \
+    case 64: return launch_out_t<T, 64>(p, st);               \
+    case 128: return launch_out_t<T, 128>(p, st);             \
+    default: return hipErrorInvalidValue;                     \
+  }
+  switch (dtype) {
+    case DT_BF16: MURM_OUT(__bf16)
+    case DT_F16: MURM_OUT(_Float16)
+    case DT_F32: MURM_OUT(float)
+    default: return hipErrorInvalidValue;
+  }
+#undef MURM_OUT
+}
+
+}  // namespace murm

@@ -181,12 +181,13 @@ def dynamic_m(N: int, M: int, slot_ratio: int = 8, m_min: int = 32) -> int:
 def murmurate_legacy(x, q_proj, k_proj, v_proj, slot_k_emb, slot_v_emb, num_heads=8,
                      rounds=3, alpha=0.9, gamma=0.15, causal=False, mask=None,
                      position_bias_fn: Optional[Callable] = None, use_dynamic_m=False,
-                     slot_ratio=8):
+                     slot_ratio=8, forced_idx=None):
     """reference.py:138-192: x, q, k, v are [B,N,D]; slot embeddings [H,M,Dh].
 
     Per round: select on q (:182-185), attend on q (:186), residual x += a
     (:187), update with the k and v projections (:188), diffusion of the
-    post-update slots (:189).  Output [B,N,D] (:191).
+    post-update slots (:189).  Output [B,N,D] (:191).  ``forced_idx`` replays
+    given per-round selections (see murmurate_readme).
     """
     B, N, D = x.shape
     H = num_heads
@@ -202,9 +203,12 @@ def murmurate_legacy(x, q_proj, k_proj, v_proj, slot_k_emb, slot_v_emb, num_head
     sk = slot_k_emb.unsqueeze(0).expand(B, -1, -1, -1)
     sv = slot_v_emb.unsqueeze(0).expand(B, -1, -1, -1)
     em = dynamic_m(N, M, slot_ratio) if use_dynamic_m else None
-    for _ in range(rounds):
+    for r in range(rounds):
         pb = position_bias_fn(xh) if position_bias_fn is not None else None
-        idx = select(qh, sk, mask=mask, causal=causal, position_bias=pb, effective_M=em)
+        if forced_idx is not None:
+            idx = forced_idx[r].to(torch.int64)
+        else:
+            idx = select(qh, sk, mask=mask, causal=causal, position_bias=pb, effective_M=em)
         a, w = attend(qh, sk, sv, idx)
         xh = xh + a
         sk, sv = update(kh, vh, sk, sv, idx, w, alpha)
@@ -213,7 +217,7 @@ def murmurate_legacy(x, q_proj, k_proj, v_proj, slot_k_emb, slot_v_emb, num_head
 
 
 def murmurate_readme(q, sk, sv, rounds=3, top_k=K_NEIGHBORS, causal=False, alpha=0.9,
-                     gamma=0.15, return_trace=False):
+                     gamma=0.15, return_trace=False, forced_idx=None):
     """README call form: slot_murmurate(q, slots_k, slots_v, rounds, top_k, causal).
 
     q [B,H,N,D]; slots [B,H,M,D].  This is reference.py:177-189 with
@@ -221,15 +225,21 @@ def murmurate_readme(q, sk, sv, rounds=3, top_k=K_NEIGHBORS, causal=False, alpha
     reference.py:152 default).  Returns (x_R, indices of the last round,
     weights of the last round) as README.md:67 documents.  With
     ``return_trace`` it also returns the per-round (sk, sv, idx, w, scores).
+    ``forced_idx`` (one [B,H,N,7] tensor per round) replaces the top-k of each
+    round: the kernel's own selections replayed, so that every other quantity
+    can be compared tightly while selection is checked on its own.
     """
     if top_k != K_NEIGHBORS:
         raise ValueError("top_k must be 7")
     x = q
     trace = []
     idx = w = None
-    for _ in range(rounds):
+    for r in range(rounds):
         s = masked_scores(q, sk, causal=causal)
-        idx = torch.topk(s, k=top_k, dim=-1, sorted=True)[1]
+        if forced_idx is not None:
+            idx = forced_idx[r].to(torch.int64)
+        else:
+            idx = torch.topk(s, k=top_k, dim=-1, sorted=True)[1]
         a, w = attend(q, sk, sv, idx)
         if return_trace:
             trace.append((sk, sv, idx, w, s.detach()))
@@ -242,7 +252,7 @@ def murmurate_readme(q, sk, sv, rounds=3, top_k=K_NEIGHBORS, causal=False, alpha
 
 
 def murmurate_backward(q, sk0, sv0, grad_out, grad_w_last=None, rounds=3, causal=False,
-                       alpha=0.9, gamma=0.15, eps=1e-8):
+                       alpha=0.9, gamma=0.15, eps=1e-8, forced_idx=None):
     """Closed-form backward of ``murmurate_readme`` (token and slot sides).
 
     Per round r, with c = 1/sqrt(D), I = idx_r, g = grad_out:
@@ -260,7 +270,7 @@ def murmurate_backward(q, sk0, sv0, grad_out, grad_w_last=None, rounds=3, causal
     M = sk0.shape[2]
     c = 1.0 / math.sqrt(D)
     _, _, _, trace = murmurate_readme(q, sk0, sv0, rounds, causal=causal, alpha=alpha,
-                                      gamma=gamma, return_trace=True)
+                                      gamma=gamma, return_trace=True, forced_idx=forced_idx)
     dq = grad_out.clone()
     Gk = torch.zeros_like(sk0)
     Gv = torch.zeros_like(sv0)

@@ -1,0 +1,314 @@
+"""GPU parity of the fused multi-round slot_murmurate (README and projection
+forms, forward and backward) against the CPU oracle, on the BASELINE configs
+and on edge shapes.  Protocol: tests/parity.py (selection checked per round
+at decided positions; everything else against the oracle replaying the
+kernel's selections)."""
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import murmurative as MA
+from murmurative import capi
+from oracle import murm_oracle as O
+from parity import TOL, assert_close, check_selection, round_indices, seeded
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _case(*a):
+    print("case", *a, flush=True)
+
+
+def run_readme(q, sk, sv, go, gw, rounds, causal, alpha=0.9, gamma=0.15):
+    """Direct op calls; returns forward results, per-round indices and grads."""
+    lib = MA.ops._get_lib()
+    B, H, N, D = q.shape
+    M = sk.shape[2]
+    out, idx, w, ws = lib.slot_murmurate_fwd(q, None, None, None, sk, sv, rounds, alpha, gamma, causal, 0,
+                                             None, None)
+    per_round = [round_indices(ws, B, H, N, D, M, rounds, True, r) for r in range(rounds - 1)] + [idx]
+    gq, _, _, gsk, gsv = lib.slot_murmurate_bwd(go, gw, q, None, None, sk, w, ws, rounds, alpha, gamma, None,
+                                               False)
+    torch.cuda.synchronize()
+    return out, idx, w, per_round, gq, gsk, gsv
+
+
+def oracle_readme(q, sk, sv, go, gw, rounds, causal, forced, alpha=0.9, gamma=0.15, dtype=torch.float64):
+    q64, sk64, sv64 = (t.detach().cpu().to(dtype).requires_grad_(True) for t in (q, sk, sv))
+    out, idx, w, trace = O.murmurate_readme(q64, sk64, sv64, rounds, causal=causal, alpha=alpha, gamma=gamma,
+                                            return_trace=True, forced_idx=[f.cpu() for f in forced])
+    grads = [go.detach().cpu().to(dtype)] + ([gw.detach().cpu().to(dtype)] if gw is not None else [])
+    torch.autograd.backward([out] + ([w] if gw is not None else []), grads)
+    return out, w, trace, q64.grad, sk64.grad, sv64.grad
+
+
+def check_readme(dtype, B, H, N, D, M, rounds=3, causal=False, seed=42, sk_std=1.0, sv_std=0.02, with_gw=True,
+                 oracle_dtype=torch.float64, alpha=0.9, gamma=0.15):
+    q, sk, sv, go = seeded([(B, H, N, D), (B, H, M, D), (B, H, M, D), (B, H, N, D)], seed,
+                           [None, sk_std, sv_std, None])
+    gw = seeded([(B, H, N, 7)], seed + 1)[0] if with_gw else None
+    q, sk, sv, go = (t.to(dtype) for t in (q, sk, sv, go))
+    dq, dsk, dsv = (t.to(DEV) for t in (q, sk, sv))
+    out, idx, w, per_round, gq, gsk, gsv = run_readme(dq, dsk, dsv, go.to(DEV),
+                                                     gw.to(DEV) if gw is not None else None, rounds, causal,
+                                                     alpha, gamma)
+    o_out, o_w, trace, o_gq, o_gsk, o_gsv = oracle_readme(q, sk, sv, go, gw, rounds, causal, per_round, alpha,
+                                                          gamma, oracle_dtype)
+    decided = [check_selection(f"round {r} indices", per_round[r], trace[r][4]) for r in range(rounds)]
+    assert torch.equal(idx.cpu(), per_round[-1].cpu())
+    res = {
+        "out": assert_close("out", out, o_out, dtype),
+        "weights": assert_close("weights", w, o_w, dtype),
+        "grad_q": assert_close("grad_q", gq, o_gq, dtype),
+        "grad_slots_k": assert_close("grad_slots_k", gsk, o_gsk, dtype),
+        "grad_slots_v": assert_close("grad_slots_v", gsv, o_gsv, dtype),
+    }
+    print("max|err|", {k: f"{v:.2e}" for k, v in res.items()}, "decided", [f"{d:.4f}" for d in decided],
+          flush=True)
+    return res
+
+
+SMALL = [
+    # dtype, B, H, N, D, M, rounds, causal
+    (torch.float32, 1, 2, 200, 64, 64, 3, False),
+    (torch.float16, 2, 2, 256, 64, 128, 3, False),
+    (torch.bfloat16, 1, 3, 333, 64, 256, 3, False),
+    (torch.bfloat16, 1, 2, 300, 32, 96, 2, True),
+    (torch.float32, 1, 2, 100, 16, 7, 3, False),
+    (torch.bfloat16, 1, 2, 128, 128, 256, 3, True),
+    (torch.float16, 1, 1, 64, 64, 512, 4, False),
+    (torch.bfloat16, 2, 1, 1100, 64, 256, 1, False),
+]
+
+
+@pytest.mark.parametrize("case", SMALL, ids=[f"s{i}" for i in range(len(SMALL))])
+def test_readme_small(case):
+    dtype, B, H, N, D, M, R, causal = case
+    _case("readme", case)
+    check_readme(dtype, B, H, N, D, M, R, causal, sv_std=0.5)
+
+
+def test_readme_alpha_gamma_variants():
+    _case("alpha/gamma")
+    check_readme(torch.float32, 1, 2, 150, 32, 48, 3, False, alpha=0.5, gamma=0.3, sv_std=1.0)
+    check_readme(torch.float32, 1, 2, 150, 32, 48, 2, False, alpha=1.0, gamma=0.0, sv_std=1.0)
+
+
+def test_autograd_api_matches_direct_ops_and_is_deterministic():
+    _case("autograd api")
+    B, H, N, D, M = 1, 4, 1000, 64, 256
+    q, sk, sv, go = seeded([(B, H, N, D), (B, H, M, D), (B, H, M, D), (B, H, N, D)], 3, [None, None, 0.02, None])
+    q, sk, sv, go = (t.to(torch.bfloat16).to(DEV) for t in (q, sk, sv, go))
+    runs = []
+    for _ in range(2):
+        qa, ska, sva = (t.clone().requires_grad_(True) for t in (q, sk, sv))
+        out, idx, w = MA.slot_murmurate(qa, ska, sva, rounds=3)
+        out.backward(go)
+        runs.append([t.detach().cpu() for t in (out, idx, w, qa.grad, ska.grad, sva.grad)])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b), "run-to-run results differ"
+    out, idx, w, _, gq, gsk, gsv = run_readme(q, sk, sv, go, None, 3, False)
+    for a, b in zip(runs[0], [out, idx, w, gq, gsk, gsv]):
+        assert torch.equal(a, b.cpu())
+
+
+def test_readme_module_layout_views():
+    # README nn.Module call: q is a transposed view, slots_k an expanded embedding
+    _case("module views")
+    B, N, H, Dh, M = 2, 256, 4, 64, 128
+    x, emb, go = seeded([(B, N, H * Dh), (H, M, Dh), (B, H, N, Dh)], 11)
+    x = x.to(torch.bfloat16).to(DEV)
+    emb = emb.to(torch.bfloat16).to(DEV).requires_grad_(True)
+    qv = x.view(B, N, H, Dh).transpose(1, 2).requires_grad_(False)
+    qv = qv.detach().requires_grad_(True)
+    sk = emb.unsqueeze(0).expand(B, -1, -1, -1)
+    sv = torch.zeros_like(sk)
+    out, idx, w = MA.slot_murmurate(qv, sk, sv, rounds=3)
+    out.backward(go.to(torch.bfloat16).to(DEV))
+    qc = qv.detach().contiguous().requires_grad_(True)
+    emb2 = emb.detach().clone().requires_grad_(True)
+    sk2 = emb2.unsqueeze(0).expand(B, -1, -1, -1).contiguous()
+    out2, idx2, w2 = MA.slot_murmurate(qc, sk2, torch.zeros_like(sk2), rounds=3)
+    out2.backward(go.to(torch.bfloat16).to(DEV))
+    assert torch.equal(out.cpu(), out2.cpu()) and torch.equal(idx.cpu(), idx2.cpu())
+    assert torch.equal(qv.grad.cpu(), qc.grad.cpu())
+    assert torch.allclose(emb.grad.float().cpu(), emb2.grad.float().cpu(), atol=2e-2)
+
+
+def test_capi_direct_call_matches_op():
+    _case("capi direct")
+    B, H, N, D, M, R = 1, 2, 300, 64, 128, 3
+    q, sk, sv = seeded([(B, H, N, D), (B, H, M, D), (B, H, M, D)], 5, [None, None, 0.1])
+    q, sk, sv = (t.to(torch.bfloat16).to(DEV) for t in (q, sk, sv))
+    lib = capi.load()
+    ws_n = lib.murm_murmurate_workspace_bytes(B, H, N, D, M, R, 1)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device=DEV)
+    out = torch.empty_like(q)
+    idx = torch.empty(B, H, N, 7, dtype=torch.int64, device=DEV)
+    w = torch.empty(B, H, N, 7, dtype=torch.float32, device=DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    P = ctypes.c_void_p
+    s = lambda t: (t.stride(0), t.stride(1), t.stride(2))  # noqa: E731
+    rc = lib.murm_murmurate_fwd(capi.BF16, capi.BF16, B, H, N, D, M, R, 0.9, 0.15, 0, 0, 0.0,
+                                P(q.data_ptr()), *s(q), None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
+                                P(sk.data_ptr()), *s(sk), P(sv.data_ptr()), *s(sv), None, 0, 0, 0, 0,
+                                P(out.data_ptr()), *s(out), P(idx.data_ptr()), P(w.data_ptr()),
+                                P(ws.data_ptr()), ws_n, P(st))
+    capi.check(rc, "murm_murmurate_fwd")
+    o2, i2, w2, _ = MA.ops._get_lib().slot_murmurate_fwd(q, None, None, None, sk, sv, R, 0.9, 0.15, False, 0,
+                                                         None, None)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), o2.cpu()) and torch.equal(idx.cpu(), i2.cpu()) and torch.equal(w.cpu(), w2.cpu())
+    # an undersized workspace is refused before launch
+    rc = lib.murm_murmurate_fwd(capi.BF16, capi.BF16, B, H, N, D, M, R, 0.9, 0.15, 0, 0, 0.0,
+                                P(q.data_ptr()), *s(q), None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
+                                P(sk.data_ptr()), *s(sk), P(sv.data_ptr()), *s(sv), None, 0, 0, 0, 0,
+                                P(out.data_ptr()), *s(out), P(idx.data_ptr()), P(w.data_ptr()),
+                                P(ws.data_ptr()), ws_n - 1, P(st))
+    assert rc == capi.ERR_ARG
+
+
+# ----------------------------------------------------------- projection form
+
+def _legacy_gpu(t, dtype):
+    return t.to(dtype).to(DEV)
+
+
+@pytest.mark.parametrize("name", ["plain", "causal", "dynm", "alpha_gamma"])
+def test_legacy_golden_fixtures(name):
+    _case("legacy golden", name)
+    d = np.load(os.path.join(GOLD, "legacy_composite.npz"))
+    B, N, H, Dh, M, R = [int(v) for v in d[name + "__meta"]]
+    kw = dict(plain={}, causal=dict(causal=True), dynm=dict(use_dynamic_m=True),
+              alpha_gamma=dict(alpha=0.5, gamma=0.3))[name]
+    t = {k: torch.from_numpy(d[f"{name}__{k}"]) for k in ("x", "q", "k", "v", "ske", "sve", "out")}
+    g = {k: _legacy_gpu(v, torch.float32) for k, v in t.items()}
+    kw.setdefault("use_dynamic_m", False)
+    out = MA.slot_murmurate(g["x"], g["q"], g["k"], g["v"], g["ske"], g["sve"], num_heads=H, rounds=R, **kw)
+    assert_close("legacy out vs golden", out, t["out"], torch.float32)
+
+
+def test_legacy_golden_mask_and_bias_fn():
+    _case("legacy golden mask+bias")
+    d = np.load(os.path.join(GOLD, "legacy_composite.npz"))
+    B, N, H, Dh, M, R = [int(v) for v in d["maskbias__meta"]]
+    t = {k: torch.from_numpy(d[f"maskbias__{k}"]) for k in ("x", "q", "k", "v", "ske", "sve", "mask", "out")}
+    g = {k: _legacy_gpu(v, torch.float32) for k, v in t.items()}
+    ramp = torch.linspace(-1.0, 1.0, M, device=DEV)
+    out = MA.slot_murmurate(g["x"], g["q"], g["k"], g["v"], g["ske"], g["sve"], num_heads=H, rounds=R,
+                            mask=g["mask"], use_dynamic_m=False,
+                            position_bias_fn=lambda xh: 0.25 * torch.tanh(xh[..., :1]) * ramp)
+    keep = torch.ones(B, N, 1, dtype=torch.bool)
+    keep[:, 5:9] = False  # fully masked tokens attend through -inf ties
+    assert_close("legacy mask+bias out", out, t["out"], torch.float32, mask=keep.expand(B, N, H * Dh))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("flags", [dict(), dict(causal=True), dict(mask=True), dict(use_dynamic_m=True)],
+                         ids=["plain", "causal", "mask", "dynm"])
+def test_legacy_fused_forward_backward(dtype, flags):
+    _case("legacy fused", dtype, flags)
+    B, N, H, Dh, M, R = 2, 160, 2, 64, 64, 3
+    D = H * Dh
+    x, q, k, v, ske, sve, go = seeded([(B, N, D)] * 4 + [(H, M, Dh), (H, M, Dh), (B, N, D)], 21,
+                                      [None, None, None, None, None, 0.5, None])
+    x, q, k, v, ske, sve, go = (t.to(dtype) for t in (x, q, k, v, ske, sve, go))
+    mask = None
+    if flags.get("mask"):
+        mask = torch.ones(B, 1, N, 1)
+        mask[:, :, 10:20] = 0
+    causal = flags.get("causal", False)
+    dyn = flags.get("use_dynamic_m", False)
+    em = O.dynamic_m(N, M) if dyn else M
+    lib = MA.ops._get_lib()
+    gx = [t.to(DEV) for t in (x, q, k, v)]
+    heads = lambda t: t.view(B, N, H, Dh).permute(0, 2, 1, 3)  # noqa: E731
+    xh, qh, kh, vh = (heads(t) for t in gx)
+    skx = ske.to(DEV).unsqueeze(0).expand(B, H, M, Dh)
+    svx = sve.to(DEV).unsqueeze(0).expand(B, H, M, Dh)
+    out, idx, w, ws = lib.slot_murmurate_fwd(qh, xh, kh, vh, skx, svx, R, 0.9, 0.15, causal, em,
+                                             None if mask is None else mask.to(DEV), None)
+    per_round = [round_indices(ws, B, H, N, Dh, M, R, False, r) for r in range(R - 1)] + [idx]
+    # autograd path gives the same forward
+    tx = [t.to(DEV).requires_grad_(True) for t in (x, q, k, v)]
+    te = [t.to(DEV).requires_grad_(True) for t in (ske, sve)]
+    y = MA.slot_murmurate(*tx, *te, num_heads=H, rounds=R, causal=causal, use_dynamic_m=dyn,
+                          mask=None if mask is None else mask.to(DEV))
+    y.backward(go.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), out.permute(0, 2, 1, 3).reshape(B, N, D).cpu())
+    o = [t.double().requires_grad_(True) for t in (x, q, k, v, ske, sve)]
+    oy = O.murmurate_legacy(*o, num_heads=H, rounds=R, causal=causal, mask=mask, use_dynamic_m=dyn,
+                            forced_idx=[p.cpu() for p in per_round])
+    oy.backward(go.double())
+    # selection per round against the replayed oracle state
+    sk_r, sv_r = ske.double().unsqueeze(0).expand(B, -1, -1, -1), sve.double().unsqueeze(0).expand(B, -1, -1, -1)
+    qh64 = heads(q.double())
+    kh64, vh64 = heads(k.double()), heads(v.double())
+    for r in range(R):
+        s = O.masked_scores(qh64, sk_r, mask=mask, causal=causal, effective_M=em if dyn else None)
+        check_selection(f"legacy round {r}", per_round[r], s)
+        _, wr = O.attend(qh64, sk_r, sv_r, per_round[r].cpu())
+        sk_r, sv_r = O.update(kh64, vh64, sk_r, sv_r, per_round[r].cpu(), wr, 0.9)
+        sk_r, sv_r = O.diffusion(sk_r, sv_r, 0.15)
+    assert_close("legacy out", y, oy, dtype)
+    for name, a, b in zip(["dx", "dq", "dk", "dv", "dslot_k", "dslot_v"], tx + te, o):
+        assert_close(f"legacy {name}", a.grad, b.grad, dtype)
+
+
+# ---------------------------------------------------------------- configs
+
+@pytest.mark.timeout(600)
+def test_config1_fp32_forward():
+    # B=2, H=4, N=128, d=64, M=256, R=3; q ~ N(0,1), slots_k ~ N(0,1), slots_v = 0
+    _case("config 1")
+    check_readme(torch.float32, 2, 4, 128, 64, 256, 3, False, sv_std=0.0, with_gw=False)
+
+
+@pytest.mark.timeout(900)
+def test_config2_fp16_forward_backward():
+    _case("config 2")
+    check_readme(torch.float16, 4, 8, 2048, 64, 256, 3, False, sv_std=0.02, with_gw=False,
+                 oracle_dtype=torch.float32)
+
+
+@pytest.mark.timeout(900)
+def test_config3_headline_bf16_forward_backward():
+    _case("config 3 (headline)")
+    check_readme(torch.bfloat16, 1, 16, 8192, 64, 256, 3, False, sk_std=1.0, sv_std=0.02, with_gw=False,
+                 oracle_dtype=torch.float32)
+
+
+@pytest.mark.timeout(900)
+def test_config4_causal_d128_subset():
+    # full-size kernel run (B=1, H=16, N=65536, d=128, causal); the oracle
+    # replays heads 0 and 15 (heads are independent)
+    _case("config 4")
+    B, H, N, D, M, R = 1, 16, 65536, 128, 256, 3
+    q, sk, sv, go = seeded([(B, H, N, D), (B, H, M, D), (B, H, M, D), (B, H, N, D)], 42, [None, None, 0.02, None])
+    dtype = torch.bfloat16
+    q, sk, sv, go = (t.to(dtype) for t in (q, sk, sv, go))
+    out, idx, w, per_round, gq, gsk, gsv = run_readme(q.to(DEV), sk.to(DEV), sv.to(DEV), go.to(DEV), None, R,
+                                                     True)
+    for h in (0, 15):
+        sl = slice(h, h + 1)
+        forced = [p[:, sl].cpu() for p in per_round]
+        o_out, o_w, trace, o_gq, o_gsk, o_gsv = oracle_readme(q[:, sl], sk[:, sl], sv[:, sl], go[:, sl], None, R,
+                                                              True, forced, dtype=torch.float32)
+        for r in range(R):
+            check_selection(f"head {h} round {r}", forced[r], trace[r][4])
+        assert_close(f"head {h} out", out[:, sl], o_out, dtype)
+        assert_close(f"head {h} weights", w[:, sl], o_w, dtype)
+        assert_close(f"head {h} grad_q", gq[:, sl], o_gq, dtype)
+        assert_close(f"head {h} grad_slots_k", gsk[:, sl], o_gsk, dtype)
+        assert_close(f"head {h} grad_slots_v", gsv[:, sl], o_gsv, dtype)
+    # size-independent properties over all heads
+    wc = w.float().cpu()
+    assert torch.allclose(wc.sum(-1), torch.ones_like(wc.sum(-1)), atol=1e-5) and (wc >= 0).all()
+    assert torch.isfinite(out.float()).all() and torch.isfinite(gq.float()).all()
