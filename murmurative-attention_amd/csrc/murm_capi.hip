@@ -141,6 +141,19 @@ struct Carve {
   }
 };
 
+// token-chunk partial sums of the slot reductions (shared by every round)
+PartParams carve_parts(Carve& c, int B, int H, int N, int D, int M) {
+  PartParams pp{};
+  pp.nchunk = seg_chunks(B, H, N, M, D);
+  if (pp.nchunk <= 0) return pp;
+  pp.chunk_tokens = seg_chunk_tokens(N, pp.nchunk);
+  const size_t BH = (size_t)B * H, S = BH * M * D;
+  pp.partA = c.take<float>(pp.nchunk * S);
+  pp.partB = c.take<float>(pp.nchunk * S);
+  pp.partW = c.take<float>(pp.nchunk * BH * M);
+  return pp;
+}
+
 struct FwdLayout {
   float* sk[MAX_ROUNDS];
   float* sv[MAX_ROUNDS];
@@ -149,6 +162,7 @@ struct FwdLayout {
   float* wsum[MAX_ROUNDS];
   uint16_t* idx[MAX_ROUNDS];
   float* w[MAX_ROUNDS];
+  PartParams part;
   size_t bytes;
 };
 FwdLayout fwd_layout(void* ws, int B, int H, int N, int D, int M, int R, int shared) {
@@ -166,6 +180,7 @@ FwdLayout fwd_layout(void* ws, int B, int H, int N, int D, int M, int R, int sha
       L.w[r] = c.take<float>(BH * N * KN);
     }
   }
+  if (R > 1) L.part = carve_parts(c, B, H, N, D, M);
   L.bytes = c.off;
   return L;
 }
@@ -175,7 +190,8 @@ struct BwdLayout {
   float* dk[MAX_ROUNDS];
   float* dv[MAX_ROUNDS];
   float* dW[MAX_ROUNDS];
-  float* Gk; float* Gv; float* ck; float* cv;
+  float* Gk; float* Gv; float* ck[2]; float* cv[2];
+  PartParams part;
   size_t bytes;
 };
 BwdLayout bwd_layout(void* ws, int B, int H, int N, int D, int M, int R, int shared) {
@@ -192,8 +208,11 @@ BwdLayout bwd_layout(void* ws, int B, int H, int N, int D, int M, int R, int sha
   }
   L.Gk = c.take<float>(S);
   L.Gv = c.take<float>(S);
-  L.ck = c.take<float>(S);
-  L.cv = c.take<float>(S);
+  for (int i = 0; i < 2; ++i) {
+    L.ck[i] = c.take<float>(S);
+    L.cv[i] = c.take<float>(S);
+  }
+  L.part = carve_parts(c, B, H, N, D, M);
   L.bytes = c.off;
   return L;
 }
@@ -203,6 +222,7 @@ struct OpLayout {   // scratch of the single-round ops
   float* K; float* V; float* W;
   float* dk; float* dv; float* dW; float* ck; float* cv;
   uint16_t* idx; float* ds; float* wtmp;
+  PartParams part;
   size_t bytes;
 };
 OpLayout op_layout(void* ws, int B, int H, int N, int D, int M, int kind) {
@@ -221,6 +241,7 @@ OpLayout op_layout(void* ws, int B, int H, int N, int D, int M, int kind) {
     L.dk = c.take<float>(S); L.dv = c.take<float>(S); L.dW = c.take<float>(BH * M);
     L.ck = c.take<float>(S); L.cv = c.take<float>(S);
   }
+  if (kind != 0) L.part = carve_parts(c, B, H, N, D, M);
   L.bytes = c.off;
   return L;
 }
@@ -451,8 +472,8 @@ int murm_select_attend_bwd(int dtype, int slot_dtype, int B, int H, int N, int D
   RUN(C_TOKB, "tok_bwd", launch_tok_bwd(dtype, DP, t, st));
   SegParams s = seg_base(B, H, N, D, M);
   s.idx = L.idx; s.wgt = weights; s.ds = L.ds; s.ds_scale = c; s.va = qv; s.vb = g;
-  s.gk_out = L.dk; s.gv_out = L.dv;
-  RUN(C_SEGB, "seg_attbwd", launch_seg(dtype, DP, SEG_ATTBWD, s, st));
+  s.final_out = 1; s.gk_out = L.dk; s.gv_out = L.dv;
+  RUN(C_SEGB, "seg_attbwd", launch_seg(dtype, DP, SEG_ATTBWD, s, &L.part, st));
   const int64_t ssb = (int64_t)H * M * D, ssh = (int64_t)M * D, ssm = D;
   RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.dk, grad_sk, ssb, ssh, ssm, B, H, M, D, st));
   RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.dv, grad_sv, ssb, ssh, ssm, B, H, M, D, st));
@@ -494,7 +515,7 @@ static int update_common(int dtype, int slot_dtype, int B, int H, int N, int D, 
   s.b_same_as_a = 0;
   s.sk_old = L.sk; s.sv_old = L.sv; s.sk_new = L.nk; s.sv_new = L.nv;
   s.alpha = (float)alpha; s.gamma = (float)gamma; s.diffuse = diffuse;
-  RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, st));
+  RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, st));
   RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.nk, sk, sk_sb, sk_sh, sk_sm, B, H, M, D, st));
   RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.nv, sv, sv_sb, sv_sh, sv_sm, B, H, M, D, st));
   return MURM_OK;
@@ -550,7 +571,7 @@ int murm_slot_update_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, 
   SegParams s = seg_base(B, H, N, D, M);
   s.idx = L.idx; s.wgt = weights; s.va = tkv; s.vb = tvv; s.b_same_as_a = 0;
   s.ksum = L.K; s.vsum = L.V; s.wsum = L.W;
-  RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, st));
+  RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, st));
   DuParams d{};
   d.B = B; d.H = H; d.M = M; d.D = D;
   d.Gk = L.sk; d.Gv = L.sv; d.K = L.K; d.V = L.V; d.W = L.W;
@@ -651,7 +672,7 @@ int murm_murmurate_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
     s.sk_old = L.sk[r]; s.sv_old = L.sv[r]; s.sk_new = L.sk[r + 1]; s.sv_new = L.sv[r + 1];
     s.ksum = L.ksum[r]; s.vsum = shared ? nullptr : L.vsum[r]; s.wsum = L.wsum[r];
     s.alpha = (float)alpha; s.gamma = (float)gamma; s.diffuse = 1;
-    RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, st));
+    RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, st));
   }
   OutParams o{};
   o.base = x ? tv_of(x, x_sb, x_sh, x_sn, dtype) : qv;
@@ -732,21 +753,25 @@ int murm_murmurate_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
     t.ds_out = G.ds[r];
     RUN(C_TOKB, "tok_bwd", launch_tok_bwd(dtype, DP, t, st));
 
+    // slot side of round r; its epilogue runs round r-1's diffusion adjoint and
+    // EMA backward (carries ping-pong: the halo rows read the other buffer)
     SegParams s = seg_base(B, H, N, D, M);
     s.idx = L.idx[r]; s.wgt = wr(r); s.ds = G.ds[r]; s.ds_scale = c; s.va = qv; s.vb = gv;
-    s.carry_k = last ? nullptr : G.ck; s.carry_v = last ? nullptr : G.cv;
-    s.gk_out = G.Gk; s.gv_out = G.Gv;
-    RUN(C_SEGB, "seg_attbwd", launch_seg(dtype, DP, SEG_ATTBWD, s, st));
-
+    s.carry_k = last ? nullptr : G.ck[(r + 1) & 1];
+    s.carry_v = last ? nullptr : G.cv[(r + 1) & 1];
     if (r > 0) {
-      DuParams d{};
-      d.B = B; d.H = H; d.M = M; d.D = D;
-      d.Gk = G.Gk; d.Gv = G.Gv; d.K = L.ksum[r - 1]; d.V = L.vsum[r - 1]; d.W = L.wsum[r - 1];
-      d.alpha = (float)alpha; d.gamma = (float)gamma; d.eps = 1e-8f; d.transpose = 1; d.combine_dk = shared;
-      d.dk_out = G.dk[r - 1]; d.dv_out = G.dv[r - 1]; d.dW_out = G.dW[r - 1];
-      d.carry_k = G.ck; d.carry_v = G.cv;
-      RUN(C_DU, "du", launch_du(d, st));
+      s.final_out = 0;
+      s.Kp = L.ksum[r - 1]; s.Vp = L.vsum[r - 1]; s.Wp = L.wsum[r - 1];
+      s.alpha = (float)alpha; s.gamma = (float)gamma;
+      s.combine_dk = shared;
+      s.dk_out = G.dk[r - 1]; s.dv_out = G.dv[r - 1]; s.dW_out = G.dW[r - 1];
+      s.carry_k_out = G.ck[r & 1]; s.carry_v_out = G.cv[r & 1];
     } else {
+      s.final_out = 1;
+      s.gk_out = G.Gk; s.gv_out = G.Gv;
+    }
+    RUN(C_SEGB, "seg_attbwd", launch_seg(dtype, DP, SEG_ATTBWD, s, &G.part, st));
+    if (r == 0) {
       const int64_t ssb = (int64_t)H * M * D, ssh = (int64_t)M * D, ssm = D;
       RUN(C_CONV, "from_state", launch_from_state(slot_dtype, G.Gk, grad_sk, ssb, ssh, ssm, B, H, M, D, st));
       RUN(C_CONV, "from_state", launch_from_state(slot_dtype, G.Gv, grad_sv, ssb, ssh, ssm, B, H, M, D, st));

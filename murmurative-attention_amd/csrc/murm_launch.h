@@ -50,8 +50,20 @@ struct SegParams {
   float alpha, gamma, eps;
   int diffuse;
   // ATTBWD
-  const float* carry_k; const float* carry_v;  // optional pass-through grads
+  const float* carry_k; const float* carry_v;  // optional pass-through grads (read, halo included)
+  int final_out;                               // 1: write G'' of the owned rows to gk_out / gv_out
   float* gk_out; float* gv_out;                // fp32 [BH, M, D]
+  // ATTBWD epilogue for the previous round (final_out == 0)
+  const float* Kp; const float* Vp; const float* Wp;  // that round's forward sums
+  int combine_dk;                              // token keys == token values: dk_out = dKk + dKv
+  float* dk_out; float* dv_out; float* dW_out;
+  float* carry_k_out; float* carry_v_out;      // must not alias carry_k / carry_v
+};
+
+struct PartParams {       // token-chunk partial sums (scratch)
+  int nchunk;             // chunks per (b,h); 0 = use the pull kernels
+  int chunk_tokens;       // tokens per chunk (multiple of the staging size)
+  float* partA; float* partB; float* partW;  // [nchunk, BH, M, D] and [nchunk, BH, M]
 };
 
 struct DuParams {
@@ -104,7 +116,9 @@ size_t sa_lds_bytes(int dtype, int DP, int M);
 hipError_t launch_attend_idx(int dtype, int DP, const AttendIdxParams& p, hipStream_t st);
 hipError_t launch_select_attend(int dtype, int DP, const SAParams& p, hipStream_t st);
 hipError_t launch_gather_out(int dtype, int DP, const OutParams& p, hipStream_t st);
-hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, hipStream_t st);
+int seg_chunks(int B, int H, int N, int M, int D);   // 0: no token-chunk path for this shape
+int seg_chunk_tokens(int N, int nchunk);
+hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp, hipStream_t st);
 hipError_t launch_du(const DuParams& p, hipStream_t st);
 hipError_t launch_tok_bwd(int dtype, int DP, const TokBwdParams& p, hipStream_t st);
 hipError_t launch_tok_grad(int dtype, int DP, const TokGradParams& p, hipStream_t st);

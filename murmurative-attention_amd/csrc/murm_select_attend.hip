@@ -205,16 +205,16 @@ __global__ __launch_bounds__(256) void sa_kernel16(SAParams p) {
     const int n = tok0 + 16 * g + col;
     uint32_t slot[KN];
     float sc[KN];
-    bool masked = false;
+    // The attend softmax uses the real q.sk of the selected slots
+    // (reference.py:56-63): re-score when a selection score was masked
+    // (causal prefix, effective_M < 7, masked token) or carried a bias.
+    bool masked = p.bias != nullptr;
 #pragma unroll
     for (int j = 0; j < KN; ++j) {
       slot[j] = key_slot(tk[g][j], p.lo_mask);
       sc[j] = key_score(tk[g][j], p.hi_mask);
       masked |= key_masked(tk[g][j]);
     }
-    // A selected slot whose selection score was masked (causal prefix,
-    // effective_M < 7, masked token) still attends with its real q.sk
-    // (reference.py:56-63): recompute those scores from the LDS keys.
     if (__any(masked)) {
       float part[KN];
 #pragma unroll

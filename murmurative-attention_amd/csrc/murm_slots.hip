@@ -1,23 +1,26 @@
 // Slot-side kernels: deterministic per-slot reductions and the small
 // per-slot epilogues.
 //
-// seg_reduce: one block owns a group of GS = 16 slots of one (b,h) (plus one
-// halo slot on each side when the forward diffusion follows).  It scans the
-// round's (token, j) -> slot entries in chunks of 1024 tokens, builds for its
-// slots a list of matching entries ordered by token (64-bit LDS bitmasks per
-// 64-token group give each entry its rank; integer OR is order-free, so the
-// list is the same on every run), and sums the token rows of each list in
-// that order with a fixed butterfly at the end.  No float atomics: the
-// result is bitwise reproducible.  Two modes:
+// seg kernels: one block (8 waves) owns a group of GS = 16 slots of one (b,h)
+// plus one halo slot on each side when a stencil follows.  It walks the
+// round's (token, j) -> slot entries in chunks of 2048 tokens: 64-bit LDS
+// bitmasks per 64-token group give every matching entry its rank (integer OR
+// is order-free), so each slot's entries land in an LDS list ordered by
+// token; the waves then gather the token rows of each list with four rows in
+// flight per lane and sum them in that order, finishing with a fixed
+// butterfly.  No float atomics: results are bitwise reproducible.
 //   UPDATE   K_m = sum w*tk, V_m = sum w*tv, W_m = sum w, then the EMA
 //            (reference.py:86-115) and, with diffusion, the stencil over the
-//            post-update rows (reference.py:118-135, 188-189).
-//   ATTBWD   dsk_m = carry_k + c * sum ds*q,  dsv_m = carry_v + sum w*g
-//            (attend backward, slot side; carry is the update backward's
-//            pass-through term).
-// du_kernel: diffusion adjoint + EMA backward for one round (per slot):
-//   G' = D^T G'', dK = (1-a)/(W+eps) G', dW = -(1-a)(K.G'k + V.G'v)/(W+eps)^2,
-//   carry = a G' on used slots, G' elsewhere.
+//            post-update rows of the block (reference.py:118-135, 188-189).
+//   ATTBWD   G''_m = carry_m + (c * sum ds*q, sum w*g): the attend backward's
+//            slot side plus the update's pass-through term, which is the
+//            gradient of the slots entering the round.  The epilogue then
+//            either writes G'' (first round) or runs the previous round's
+//            diffusion adjoint and EMA backward on it (halo rows supply the
+//            stencil neighbours):
+//              G' = D^T G'', dK = (1-a)/(W+eps) G', carry = a G' (used) | G',
+//              dW = -(1-a)(K.G'k + V.G'v)/(W+eps)^2.
+// du_kernel: the same EMA backward for the standalone update op.
 
 #include "murm_common.h"
 #include "murm_launch.h"
@@ -26,25 +29,48 @@ namespace murm {
 
 namespace {
 
-constexpr int GS = 16;             // owned slots per block
-constexpr int NSMAX = GS + 2;      // with halo
-constexpr int CH = 1024;           // tokens per chunk
-constexpr int NGRP = CH / 64;      // 64-token groups per chunk
-constexpr int SPW = (NSMAX + 3) / 4;  // slots per wave (round robin)
+constexpr int GS = 16;                 // owned slots per block
+constexpr int NSMAX = GS + 2;          // with halo
+constexpr int SEG_THREADS = 512;
+constexpr int SEG_WAVES = SEG_THREADS / 64;
+constexpr int CH = 4096;               // tokens per chunk (entry = token-local << 3 | j fits u16)
+constexpr int NGRP = CH / 64;          // 64-token groups per chunk (one per lane in the scans)
+static_assert(NGRP == 64, "the group prefix scan maps one group per lane");
+constexpr int TPT = CH / SEG_THREADS;  // tokens per thread in the scan
+constexpr int SPW = (NSMAX + SEG_WAVES - 1) / SEG_WAVES;  // slots per wave
+constexpr int UNR = 4;                 // rows in flight per lane
 
 struct SegShared {
   unsigned long long masks[NGRP][NSMAX];
   uint16_t goff[NGRP][NSMAX];
   int cnt[NSMAX];
   int loff[NSMAX];
-  uint16_t list[CH * IDX_ROW];
+  uint16_t list[CH * KN];
 };
+
+__device__ __forceinline__ uint32_t idx_at(const uint4& r, int j) {
+  const uint32_t w = j < 2 ? r.x : (j < 4 ? r.y : (j < 6 ? r.z : r.w));
+  return (w >> (16 * (j & 1))) & 0xFFFF;
+}
+
+// 1-D grid, XCD-aware: workgroups are dispatched round-robin over the 8 XCDs
+// (linear id % 8), so every block of one (b,h) is placed on XCD bh % 8 and
+// the head's token rows, gathered about seven times over, stay in that
+// XCD's L2.  Blocks past the last head return before any barrier.
+constexpr int XCDS = 8;
+__device__ __forceinline__ bool seg_block(const SegParams& p, int& bh, int& g0) {
+  const int G = (p.M + GS - 1) / GS;
+  const int L = blockIdx.x, x = L % XCDS, k = L / XCDS;
+  bh = x + XCDS * (k / G);
+  g0 = (k % G) * GS;
+  return bh < p.B * p.H;
+}
 
 template <typename T, int DP, int MODE>
 __device__ void seg_accumulate(const SegParams& p, int bh, int lo, int NS, SegShared& sh,
                                float* accA, float* accB, float* accW) {
-  constexpr int DCH = DP / 8;        // 8-dim chunks
-  constexpr int ES = 64 / DCH;       // entries in flight per wave
+  constexpr int DCH = DP / 8;        // 8-dim chunks per row
+  constexpr int ES = 64 / DCH;       // rows per wave step
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int es = lane / DCH, dc = lane % DCH;
   const int d0 = dc * 8;
@@ -62,86 +88,105 @@ __device__ void seg_accumulate(const SegParams& p, int bh, int lo, int NS, SegSh
   const uint16_t* idxb = p.idx + (int64_t)bh * p.N * IDX_ROW;
   const float* wb = p.wgt + (int64_t)bh * p.N * p.K;
   const float* db = (MODE == SEG_ATTBWD) ? p.ds + (int64_t)bh * p.N * p.K : nullptr;
+  const unsigned long long below = (1ull << lane) - 1ull;
 
   for (int c0 = 0; c0 < p.N; c0 += CH) {
-    for (int i = tid; i < NGRP * NSMAX; i += blockDim.x) (&sh.masks[0][0])[i] = 0ull;
+    for (int i = tid; i < NGRP * NSMAX; i += SEG_THREADS) (&sh.masks[0][0])[i] = 0ull;
     __syncthreads();
-    uint4 rows[CH / 256];
+    uint4 rows[TPT];
 #pragma unroll
-    for (int i = 0; i < CH / 256; ++i) {
-      const int n = c0 + i * 256 + tid;
+    for (int i = 0; i < TPT; ++i) {
+      const int n = c0 + i * SEG_THREADS + tid;
       rows[i] = (n < p.N) ? *reinterpret_cast<const uint4*>(idxb + (int64_t)n * IDX_ROW)
                           : make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
-      const uint32_t wv[4] = {rows[i].x, rows[i].y, rows[i].z, rows[i].w};
-      const int grp = i * 4 + wave;
+      const int grp = i * SEG_WAVES + wave;
 #pragma unroll
-      for (int j = 0; j < KN + 1; ++j) {
-        if (j >= p.K) break;
-        const uint32_t s = (wv[j >> 1] >> (16 * (j & 1))) & 0xFFFF;
+      for (int j = 0; j < KN; ++j) {
+        const uint32_t s = idx_at(rows[i], j);
         const uint32_t rel = s - (uint32_t)lo;
         if (s != IDX_NONE && rel < (uint32_t)NS) atomicOr(&sh.masks[grp][rel], 1ull << lane);
       }
     }
     __syncthreads();
-    if (tid < NS) {
-      int run = 0;
-      for (int g = 0; g < NGRP; ++g) {
-        sh.goff[g][tid] = (uint16_t)run;
-        run += __popcll(sh.masks[g][tid]);
+    // per slot: exclusive scan of the group popcounts (one group per lane)
+    for (int s = wave; s < NS; s += SEG_WAVES) {
+      const int c = __popcll(sh.masks[lane][s]);
+      int incl = c;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += t;
       }
-      sh.cnt[tid] = run;
+      sh.goff[lane][s] = (uint16_t)(incl - c);
+      if (lane == 63) sh.cnt[s] = incl;
     }
     __syncthreads();
-    if (tid == 0) {
-      int o = 0;
-      for (int s = 0; s < NS; ++s) { sh.loff[s] = o; o += sh.cnt[s]; }
+    if (wave == 0) {  // slot offsets: exclusive scan over the NS counts
+      const int c = lane < NS ? sh.cnt[lane] : 0;
+      int incl = c;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += t;
+      }
+      if (lane < NS) sh.loff[lane] = incl - c;
     }
     __syncthreads();
-    const unsigned long long below = (1ull << lane) - 1ull;
 #pragma unroll
-    for (int i = 0; i < CH / 256; ++i) {
-      const uint32_t wv[4] = {rows[i].x, rows[i].y, rows[i].z, rows[i].w};
-      const int grp = i * 4 + wave;
+    for (int i = 0; i < TPT; ++i) {
+      const int grp = i * SEG_WAVES + wave;
 #pragma unroll
-      for (int j = 0; j < KN + 1; ++j) {
-        if (j >= p.K) break;
-        const uint32_t s = (wv[j >> 1] >> (16 * (j & 1))) & 0xFFFF;
+      for (int j = 0; j < KN; ++j) {
+        const uint32_t s = idx_at(rows[i], j);
         const uint32_t rel = s - (uint32_t)lo;
         if (s != IDX_NONE && rel < (uint32_t)NS) {
           const int pos = sh.loff[rel] + sh.goff[grp][rel] + __popcll(sh.masks[grp][rel] & below);
-          sh.list[pos] = (uint16_t)(((i * 256 + tid) << 3) | j);
+          sh.list[pos] = (uint16_t)(((i * SEG_THREADS + tid) << 3) | j);
         }
       }
     }
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < SPW; ++s) {
-      const int rel = wave + 4 * s;
+      const int rel = wave + SEG_WAVES * s;
       if (rel >= NS) break;
       const int beg = sh.loff[rel], end = beg + sh.cnt[rel];
-      for (int e = beg + es; e < end; e += ES) {
-        const uint32_t ent = sh.list[e];
-        const int n = c0 + (int)(ent >> 3);
-        const int j = (int)(ent & 7);
-        const float w = wb[(int64_t)n * p.K + j];
-        float va[8];
-        load8<T>(tok_row<T>(p.va, b, h, n), d0, p.D, p.va.vec, va);
-        if constexpr (MODE == SEG_UPDATE) {
+      for (int e0 = beg + es; e0 < end; e0 += ES * UNR) {
+        int nn[UNR], jj[UNR];
+        bool ok[UNR];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) aA[s][i] += w * va[i];
-          aW[s] += w;
-          if (!sameB) {
-            float vb[8];
-            load8<T>(tok_row<T>(p.vb, b, h, n), d0, p.D, p.vb.vec, vb);
+        for (int u = 0; u < UNR; ++u) {
+          const int e = e0 + u * ES;
+          ok[u] = e < end;
+          const uint32_t ent = ok[u] ? sh.list[e] : 0u;
+          nn[u] = c0 + (int)(ent >> 3);
+          jj[u] = (int)(ent & 7);
+        }
+        float ca[UNR], cb[UNR], va[UNR][8], vb[UNR][8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) aB[s][i] += w * vb[i];
+        for (int u = 0; u < UNR; ++u) {
+          if (ok[u]) {
+            const int64_t o = (int64_t)nn[u] * p.K + jj[u];
+            cb[u] = wb[o];
+            ca[u] = (MODE == SEG_ATTBWD) ? p.ds_scale * db[o] : cb[u];
+            load8<T>(tok_row<T>(p.va, b, h, nn[u]), d0, p.D, p.va.vec, va[u]);
+            if (!sameB) load8<T>(tok_row<T>(p.vb, b, h, nn[u]), d0, p.D, p.vb.vec, vb[u]);
+          } else {
+            ca[u] = 0.f;
+            cb[u] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { va[u][i] = 0.f; vb[u][i] = 0.f; }
           }
-        } else {
-          const float ca = p.ds_scale * db[(int64_t)n * p.K + j];
-          float vb[8];
-          load8<T>(tok_row<T>(p.vb, b, h, n), d0, p.D, p.vb.vec, vb);
+        }
 #pragma unroll
-          for (int i = 0; i < 8; ++i) { aA[s][i] += ca * va[i]; aB[s][i] += w * vb[i]; }
+        for (int u = 0; u < UNR; ++u) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) aA[s][i] += ca[u] * va[u][i];
+          if (!sameB) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) aB[s][i] += cb[u] * vb[u][i];
+          }
+          if (MODE == SEG_UPDATE) aW[s] += cb[u];
         }
       }
     }
@@ -151,7 +196,7 @@ __device__ void seg_accumulate(const SegParams& p, int bh, int lo, int NS, SegSh
   // fixed butterfly over the entry lanes, then lanes with es == 0 publish
 #pragma unroll
   for (int s = 0; s < SPW; ++s) {
-    const int rel = wave + 4 * s;
+    const int rel = wave + SEG_WAVES * s;
 #pragma unroll
     for (int x = DCH; x < 64; x <<= 1) {
       aW[s] += shfl_xor_f(aW[s], x);
@@ -173,17 +218,14 @@ __device__ void seg_accumulate(const SegParams& p, int bh, int lo, int NS, SegSh
   __syncthreads();
 }
 
-template <typename T, int DP>
-__global__ __launch_bounds__(256) void seg_update_kernel(SegParams p) {
-  __shared__ SegShared sh;
-  __shared__ float accA[NSMAX * DP], accB[NSMAX * DP], accW[NSMAX];
-  const int bh = blockIdx.y;
-  const int g0 = blockIdx.x * GS;
-  const int halo = p.diffuse ? 1 : 0;
+// ---------------------------------------------------------------------------
+// Epilogues (shared by the pull kernels and the partial-sum reduction).  The
+// block holds, in LDS, the sums of rows lo .. lo+NS-1 (lo = g0 - halo).
+// ---------------------------------------------------------------------------
+template <int DP>
+__device__ void update_epilogue(const SegParams& p, int bh, int g0, int halo, int NS, float* accA, float* accB,
+                                const float* accW) {
   const int lo = g0 - halo;
-  const int NS = GS + 2 * halo;
-  seg_accumulate<T, DP, SEG_UPDATE>(p, bh, lo, NS, sh, accA, accB, accW);
-
   const int64_t base = (int64_t)bh * p.M * p.D;
   const float a = p.alpha, oma = 1.0f - p.alpha;
   // raw sums of the owned rows (kept for the backward)
@@ -229,30 +271,381 @@ __global__ __launch_bounds__(256) void seg_update_kernel(SegParams p) {
   }
 }
 
+template <int DP>
+__device__ void attbwd_epilogue(const SegParams& p, int bh, int g0, int halo, int NS, float* accA, float* accB) {
+  const int lo = g0 - halo;
+  const int64_t base = (int64_t)bh * p.M * p.D;
+  // G'' rows (owned + halo)
+  for (int i = threadIdx.x; i < NS * DP; i += blockDim.x) {
+    const int rel = i / DP, d = i % DP, m = lo + rel;
+    if (m < 0 || m >= p.M || d >= p.D) continue;
+    const int64_t o = base + (int64_t)m * p.D + d;
+    accA[i] += p.carry_k ? p.carry_k[o] : 0.f;
+    accB[i] += p.carry_v ? p.carry_v[o] : 0.f;
+  }
+  __syncthreads();
+  if (p.final_out) {
+    for (int i = threadIdx.x; i < GS * DP; i += blockDim.x) {
+      const int own = i / DP, d = i % DP, m = g0 + own;
+      if (m >= p.M || d >= p.D) continue;
+      const int64_t o = base + (int64_t)m * p.D + d;
+      p.gk_out[o] = accA[(own + halo) * DP + d];
+      p.gv_out[o] = accB[(own + halo) * DP + d];
+    }
+    return;
+  }
+  // previous round's diffusion adjoint + EMA backward on the owned rows:
+  // 32 threads per slot, DP/32 dims each (DP >= 32); uniform per 32-lane group
+  constexpr int DPT = DP / 32;
+  const int sub = threadIdx.x & 31;
+  const float g = p.gamma, a = p.alpha, oma = 1.0f - p.alpha;
+  auto inner = [&](int x) { return p.M >= 3 && x >= 1 && x <= p.M - 2; };
+  for (int own = threadIdx.x >> 5; own < GS; own += blockDim.x >> 5) {
+    const int m = g0 + own, rel = own + halo;
+    const bool live = m < p.M;
+    const float W = live ? p.Wp[(int64_t)bh * p.M + m] : 0.f;
+    const bool used = W > 0.f;
+    const float inv = oma / (W + p.eps);
+    float dot = 0.f;
+#pragma unroll
+    for (int t = 0; t < DPT; ++t) {
+      const int d = sub + 32 * t;
+      if (!live || d >= p.D) continue;
+      auto adj = [&](const float* G) {
+        const float c = G[rel * DP + d];
+        float r = c;
+        if (inner(m)) r -= 2.0f * g * c;
+        if (inner(m - 1)) r += g * G[(rel - 1) * DP + d];
+        if (inner(m + 1)) r += g * G[(rel + 1) * DP + d];
+        return r;
+      };
+      const float gk = adj(accA), gv = adj(accB);
+      const int64_t o = base + (int64_t)m * p.D + d;
+      if (used) dot += p.Kp[o] * gk + p.Vp[o] * gv;
+      const float dk = used ? inv * gk : 0.f, dv = used ? inv * gv : 0.f;
+      if (p.combine_dk) {
+        p.dk_out[o] = dk + dv;
+      } else {
+        p.dk_out[o] = dk;
+        p.dv_out[o] = dv;
+      }
+      p.carry_k_out[o] = used ? a * gk : gk;
+      p.carry_v_out[o] = used ? a * gv : gv;
+    }
+#pragma unroll
+    for (int x = 1; x < 32; x <<= 1) dot += shfl_xor_f(dot, x);
+    if (live && sub == 0) {
+      const float den = W + p.eps;
+      p.dW_out[(int64_t)bh * p.M + m] = used ? -oma * dot / (den * den) : 0.f;
+    }
+  }
+}
+
+// pull kernels: one block owns GS slots (+halo) and gathers their entries
 template <typename T, int DP>
-__global__ __launch_bounds__(256) void seg_attbwd_kernel(SegParams p) {
+__global__ __launch_bounds__(SEG_THREADS) void seg_update_kernel(SegParams p) {
   __shared__ SegShared sh;
   __shared__ float accA[NSMAX * DP], accB[NSMAX * DP], accW[NSMAX];
-  const int bh = blockIdx.y;
-  const int g0 = blockIdx.x * GS;
-  seg_accumulate<T, DP, SEG_ATTBWD>(p, bh, g0, GS, sh, accA, accB, accW);
-  const int64_t base = (int64_t)bh * p.M * p.D;
-  for (int i = threadIdx.x; i < GS * DP; i += blockDim.x) {
-    const int own = i / DP, d = i % DP, m = g0 + own;
-    if (m >= p.M || d >= p.D) continue;
-    const int64_t o = base + (int64_t)m * p.D + d;
-    p.gk_out[o] = (p.carry_k ? p.carry_k[o] : 0.f) + accA[i];
-    p.gv_out[o] = (p.carry_v ? p.carry_v[o] : 0.f) + accB[i];
+  int bh, g0;
+  if (!seg_block(p, bh, g0)) return;
+  const int halo = p.diffuse ? 1 : 0;
+  seg_accumulate<T, DP, SEG_UPDATE>(p, bh, g0 - halo, GS + 2 * halo, sh, accA, accB, accW);
+  update_epilogue<DP>(p, bh, g0, halo, GS + 2 * halo, accA, accB, accW);
+}
+
+template <typename T, int DP>
+__global__ __launch_bounds__(SEG_THREADS) void seg_attbwd_kernel(SegParams p) {
+  __shared__ SegShared sh;
+  __shared__ float accA[NSMAX * DP], accB[NSMAX * DP], accW[NSMAX];
+  int bh, g0;
+  if (!seg_block(p, bh, g0)) return;
+  const int halo = p.final_out ? 0 : 1;
+  seg_accumulate<T, DP, SEG_ATTBWD>(p, bh, g0 - halo, GS + 2 * halo, sh, accA, accB, accW);
+  attbwd_epilogue<DP>(p, bh, g0, halo, GS + 2 * halo, accA, accB);
+}
+
+// ---------------------------------------------------------------------------
+// Token-chunk path.
+// seg_partial: one block owns a token range of one (b,h) and every slot of
+// that head; thread (slot, vector, part) accumulates DP/TPS dims of one slot
+// sum in registers.  The range is walked in sub-chunks of SUB tokens: the
+// token rows (16-byte units, coalesced), index rows and coefficient rows are
+// staged in LDS while the next sub-chunk's loads are already in flight in
+// registers; each token sets its slots' bits in 64-bit LDS masks (integer OR:
+// order-free); every thread then walks its slot's bits in token order and
+// reads index, coefficients and row of a token with independent LDS loads.
+// The block writes one partial sum per slot.
+// seg_reduce: adds the partials of a slot group in chunk order, then runs
+// the update or attend-backward epilogue.
+// Blocks of one (b,h) run on one XCD (1-D grid, linear id % 8 = XCD), so the
+// partials are re-read from that XCD's L2.
+// ---------------------------------------------------------------------------
+constexpr int SUB = 128;    // tokens per staged sub-chunk
+constexpr int PF = 2;       // 16-byte row units prefetched per thread
+constexpr int CW = 8;       // coefficient row (7 used)
+constexpr int NCMAX = 16;   // chunks per (b,h)
+
+template <typename T>
+__device__ __forceinline__ uint4 load_unit(const TokView& v, int b, int h, int n, int e0, int D) {
+  constexpr int E = 16 / sizeof(T);
+  const T* row = tok_row<T>(v, b, h, n);
+  if (v.vec && e0 + E <= D) return *reinterpret_cast<const uint4*>(row + e0);
+  uint4 r;
+  T* e = reinterpret_cast<T*>(&r);
+#pragma unroll
+  for (int i = 0; i < E; ++i) e[i] = (e0 + i < D) ? row[e0 + i] : from_f<T>(0.f);
+  return r;
+}
+
+__device__ __forceinline__ void part_block(int nchunk, int BH, int& bh, int& chunk) {
+  const int L = blockIdx.x, x = L % XCDS, k = L / XCDS;
+  bh = x + XCDS * (k / nchunk);
+  chunk = k % nchunk;
+  if (bh >= BH) bh = -1;
+}
+
+template <typename T, int DP, int TPS>
+__device__ __forceinline__ void fma_row(float (&acc)[DP / TPS], float c, const uint4 (&x)[DP / TPS * sizeof(T) / 16]) {
+  constexpr int DPT = DP / TPS, E = 16 / sizeof(T);
+#pragma unroll
+  for (int u = 0; u < DPT / E; ++u) {
+    const T* e = reinterpret_cast<const T*>(&x[u]);
+#pragma unroll
+    for (int i = 0; i < E; ++i) acc[u * E + i] += c * to_f(e[i]);
   }
+}
+
+template <typename T, int DP, int TPS, int MODE>
+__global__ __launch_bounds__(DP / TPS <= 32 ? 1024 : 512) void seg_partial_kernel(SegParams p, PartParams pp) {
+  constexpr int ROW = DP + 8;                 // staged row stride (elements; bytes % 16 == 0)
+  constexpr int DPT = DP / TPS;               // dims per thread
+  constexpr int E = 16 / sizeof(T);           // elements per 16-byte unit
+  constexpr int UPR = DP / E;                 // units per staged row
+  constexpr int UPT = DPT / E;                // units per thread and token
+  extern __shared__ __align__(16) unsigned char smem[];
+  const bool sameB = (MODE == SEG_UPDATE) && p.b_same_as_a;
+  const int nvec = sameB ? 1 : 2;
+  const int Mp = (p.M + 63) & ~63;
+  T* rows = reinterpret_cast<T*>(smem);                                   // [nvec][SUB][ROW]
+  uint4* idxs = reinterpret_cast<uint4*>(rows + nvec * SUB * ROW);        // [SUB]
+  float* cw = reinterpret_cast<float*>(idxs + SUB);                       // [SUB][CW] weights
+  float* cd = cw + SUB * CW;                                              // [SUB][CW] c * ds
+  unsigned long long* masks =
+      reinterpret_cast<unsigned long long*>(cd + (MODE == SEG_ATTBWD ? SUB * CW : 0));  // [SUB/64][Mp]
+
+  int bh, chunk;
+  part_block(pp.nchunk, p.B * p.H, bh, chunk);
+  if (bh < 0) return;  // whole block, before any barrier
+  const int b = bh / p.H, h = bh % p.H;
+  const int c_beg = chunk * pp.chunk_tokens;
+  const int c_end = min(p.N, c_beg + pp.chunk_tokens);
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int part = tid % TPS;
+  const int vec = (tid / TPS) % nvec;
+  const int slot = tid / (TPS * nvec);
+  const bool own = slot < p.M;
+  const int nunits = nvec * SUB * UPR;
+
+  uint4 pf[PF];
+  uint4 pidx;
+  float pw[2], pd[2];
+  // global -> registers (the first PF units per thread, one index row, two coefficients)
+  auto fetch = [&](int n0) {
+    const int cnt = min(SUB, c_end - n0);
+#pragma unroll
+    for (int k = 0; k < PF; ++k) {
+      const int u = tid + k * nthr;
+      pf[k] = make_uint4(0u, 0u, 0u, 0u);
+      const int v = u / (SUB * UPR), r = (u / UPR) % SUB, c = u % UPR;
+      if (u < nunits && r < cnt) pf[k] = load_unit<T>(v == 0 ? p.va : p.vb, b, h, n0 + r, c * E, p.D);
+    }
+    const int64_t row0 = (int64_t)bh * p.N + n0;
+    pidx = make_uint4(~0u, ~0u, ~0u, ~0u);
+    if (tid < cnt) pidx = *reinterpret_cast<const uint4*>(p.idx + (row0 + tid) * IDX_ROW);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int i = tid + k * nthr, t = i / CW, j = i % CW;
+      const bool in = i < SUB * CW && t < cnt && j < KN;
+      pw[k] = in ? p.wgt[(row0 + t) * KN + j] : 0.f;
+      pd[k] = (MODE == SEG_ATTBWD && in) ? p.ds_scale * p.ds[(row0 + t) * KN + j] : 0.f;
+    }
+  };
+  // registers -> LDS, plus whatever the registers did not cover (small blocks)
+  auto stash = [&](int n0) {
+    const int cnt = min(SUB, c_end - n0);
+    const int64_t row0 = (int64_t)bh * p.N + n0;
+#pragma unroll
+    for (int k = 0; k < PF; ++k) {
+      const int u = tid + k * nthr;
+      const int v = u / (SUB * UPR), r = (u / UPR) % SUB, c = u % UPR;
+      if (u < nunits) *reinterpret_cast<uint4*>(rows + (v * SUB + r) * ROW + c * E) = pf[k];
+    }
+    for (int u = tid + PF * nthr; u < nunits; u += nthr) {
+      const int v = u / (SUB * UPR), r = (u / UPR) % SUB, c = u % UPR;
+      *reinterpret_cast<uint4*>(rows + (v * SUB + r) * ROW + c * E) =
+          r < cnt ? load_unit<T>(v == 0 ? p.va : p.vb, b, h, n0 + r, c * E, p.D) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (tid < SUB) idxs[tid] = pidx;
+    for (int i = tid + nthr; i < SUB; i += nthr)
+      idxs[i] = i < cnt ? *reinterpret_cast<const uint4*>(p.idx + (row0 + i) * IDX_ROW)
+                        : make_uint4(~0u, ~0u, ~0u, ~0u);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int i = tid + k * nthr;
+      if (i < SUB * CW) {
+        cw[i] = pw[k];
+        if (MODE == SEG_ATTBWD) cd[i] = pd[k];
+      }
+    }
+    for (int i = tid + 2 * nthr; i < SUB * CW; i += nthr) {
+      const int t = i / CW, j = i % CW;
+      const bool in = t < cnt && j < KN;
+      cw[i] = in ? p.wgt[(row0 + t) * KN + j] : 0.f;
+      if (MODE == SEG_ATTBWD) cd[i] = in ? p.ds_scale * p.ds[(row0 + t) * KN + j] : 0.f;
+    }
+    for (int i = tid; i < (SUB / 64) * Mp; i += nthr) masks[i] = 0ull;
+  };
+
+  float acc[DPT];
+#pragma unroll
+  for (int i = 0; i < DPT; ++i) acc[i] = 0.f;
+  float accw = 0.f;
+  const T* vrows = rows + vec * SUB * ROW + part * DPT;
+  const float* coef = (MODE == SEG_ATTBWD && vec == 0) ? cd : cw;
+  const bool wacc = (MODE == SEG_UPDATE) && vec == 0 && part == 0;
+  const uint32_t me = (uint32_t)slot;
+  // coefficient of this slot in token t: the sum over every j that names it
+  // (more than one j only with caller-given indices), in j order
+  auto coef_of = [&](int t, const uint4& ir) {
+    uint32_t mb = 0;
+#pragma unroll
+    for (int j = 0; j < KN; ++j) mb |= (idx_at(ir, j) == me ? 1u : 0u) << j;
+    float c = coef[t * CW + __builtin_ctz(mb | 0x80u)];
+    for (uint32_t r = mb & (mb - 1u); r; r &= r - 1u) c += coef[t * CW + __builtin_ctz(r)];
+    return c;
+  };
+  auto row_of = [&](int t, uint4 (&x)[UPT]) {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) x[u] = *reinterpret_cast<const uint4*>(vrows + t * ROW + u * E);
+  };
+
+  fetch(c_beg);
+  for (int n0 = c_beg; n0 < c_end; n0 += SUB) {
+    const int cnt = min(SUB, c_end - n0);
+    stash(n0);
+    __syncthreads();
+    if (n0 + SUB < c_end) fetch(n0 + SUB);  // in flight during marking and the walk
+    for (int t = tid; t < cnt; t += nthr) {
+      const uint4 ir = idxs[t];
+#pragma unroll
+      for (int j = 0; j < KN; ++j) {
+        const uint32_t s = idx_at(ir, j);
+        if (s < (uint32_t)p.M) atomicOr(&masks[(t >> 6) * Mp + s], 1ull << (t & 63));
+      }
+    }
+    __syncthreads();
+    if (own) {
+#pragma unroll
+      for (int g = 0; g < SUB / 64; ++g) {
+        unsigned long long mk = masks[g * Mp + slot];
+        while (mk) {
+          const int t = g * 64 + (int)__builtin_ctzll(mk);
+          mk &= mk - 1ull;
+          uint4 x[UPT];
+          const uint4 ir = idxs[t];
+          row_of(t, x);
+          const float a = coef_of(t, ir);
+          fma_row<T, DP, TPS>(acc, a, x);
+          if (wacc) accw += a;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (!own) return;
+  const int64_t prow = ((int64_t)chunk * p.B * p.H + bh) * p.M + slot;
+  float* dst = (vec == 0 ? pp.partA : pp.partB) + prow * p.D + part * DPT;
+  if ((p.D & 3) == 0 && part * DPT + DPT <= p.D) {
+#pragma unroll
+    for (int i = 0; i < DPT; i += 4)
+      *reinterpret_cast<float4*>(dst + i) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < DPT; ++i)
+      if (part * DPT + i < p.D) dst[i] = acc[i];
+  }
+  if (wacc) pp.partW[prow] = accw;
+}
+
+template <int DP, int MODE>
+__global__ __launch_bounds__(256) void seg_reduce_kernel(SegParams p, PartParams pp) {
+  __shared__ float accA[NSMAX * DP], accB[NSMAX * DP], accW[NSMAX];
+  int bh, g0;
+  if (!seg_block(p, bh, g0)) return;
+  const int halo = (MODE == SEG_UPDATE) ? (p.diffuse ? 1 : 0) : (p.final_out ? 0 : 1);
+  const int lo = g0 - halo, NS = GS + 2 * halo;
+  const bool sameB = (MODE == SEG_UPDATE) && p.b_same_as_a;
+  const int nv = sameB ? 1 : 2;
+  const int64_t cstride = (int64_t)p.B * p.H * p.M * p.D;
+  const int nc = pp.nchunk;
+  constexpr int QPR = DP / 4;
+  // quads of 4 dims: all chunk loads of a quad are issued before the adds
+  for (int i = threadIdx.x; i < nv * NS * QPR; i += blockDim.x) {
+    const int v = i / (NS * QPR), rel = (i / QPR) % NS, d = (i % QPR) * 4, m = lo + rel;
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (m >= 0 && m < p.M && d < p.D) {
+      const float* src = (v == 0 ? pp.partA : pp.partB) + ((int64_t)bh * p.M + m) * p.D + d;
+      if ((p.D & 3) == 0) {
+        float4 x[NCMAX];
+#pragma unroll
+        for (int c = 0; c < NCMAX; ++c)
+          x[c] = c < nc ? *reinterpret_cast<const float4*>(src + c * cstride) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int c = 0; c < NCMAX; ++c) {
+          if (c < nc) {
+            sum.x += x[c].x; sum.y += x[c].y; sum.z += x[c].z; sum.w += x[c].w;
+          }
+        }
+      } else {
+        float t[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < nc; ++c)
+          for (int e = 0; e < 4; ++e)
+            if (d + e < p.D) t[e] += src[c * cstride + e];
+        sum = make_float4(t[0], t[1], t[2], t[3]);
+      }
+    }
+    float* acc = (v == 0 ? accA : accB) + rel * DP + d;
+    acc[0] = sum.x; acc[1] = sum.y; acc[2] = sum.z; acc[3] = sum.w;
+    if (sameB) {
+      float* accb = accB + rel * DP + d;
+      accb[0] = sum.x; accb[1] = sum.y; accb[2] = sum.z; accb[3] = sum.w;
+    }
+  }
+  if (MODE == SEG_UPDATE) {
+    for (int rel = threadIdx.x; rel < NS; rel += blockDim.x) {
+      const int m = lo + rel;
+      float sw = 0.f;
+      if (m >= 0 && m < p.M)
+        for (int c = 0; c < nc; ++c) sw += pp.partW[((int64_t)c * p.B * p.H + bh) * p.M + m];
+      accW[rel] = sw;
+    }
+  }
+  __syncthreads();
+  if (MODE == SEG_UPDATE)
+    update_epilogue<DP>(p, bh, g0, halo, NS, accA, accB, accW);
+  else
+    attbwd_epilogue<DP>(p, bh, g0, halo, NS, accA, accB);
 }
 
 // One block per (b,h): G' = D^T G'' (optional), then the EMA backward.
 __global__ __launch_bounds__(256) void du_kernel(DuParams p) {
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.y;
   const int64_t base = (int64_t)bh * p.M * p.D;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float g = p.gamma, a = p.alpha, oma = 1.0f - p.alpha;
-  for (int m = wave; m < p.M; m += 4) {
+  {
+    const int m = blockIdx.x * 4 + wave;
+    if (m >= p.M) return;
     float dot = 0.f;
     const float W = p.W[(int64_t)bh * p.M + m];
     const bool used = W > 0.f;
@@ -389,13 +782,65 @@ __global__ void stencil_kernel(T* __restrict__ x, int64_t sb, int64_t sh, int64_
   }
 }
 
+// Threads per (slot, vector) of the token-chunk path: 32 dims each when the
+// block fits 1024 threads, else 64 dims each in at most 512 threads (register
+// budget); 0 = use the pull kernels.
+int part_tps(int DP, int M, int nvec) {
+  const int Mp = (M + 63) & ~63;
+  if (Mp * nvec * (DP / 32) <= 1024) return DP / 32;              // 32 dims per thread
+  if (DP >= 64 && Mp * nvec * (DP / 64) <= 512) return DP / 64;   // 64 dims, 512 threads at most
+  return 0;
+}
+
 template <typename T, int DP>
-hipError_t launch_seg_t(const SegParams& p, int mode, hipStream_t st) {
-  dim3 grid((p.M + GS - 1) / GS, p.B * p.H);
+size_t part_lds_bytes(int M, int mode, int nvec) {
+  const size_t Mp = (size_t)((M + 63) & ~63);
+  return (size_t)nvec * SUB * (DP + 8) * sizeof(T) + SUB * 16 + (size_t)SUB * CW * 4 * (mode == SEG_ATTBWD ? 2 : 1) +
+         (SUB / 64) * Mp * 8;
+}
+
+template <typename T, int DP, int TPS, int MODE>
+hipError_t launch_part(const SegParams& p, const PartParams& pp, int nvec, size_t lds, hipStream_t st) {
+  const void* fn = reinterpret_cast<const void*>(&seg_partial_kernel<T, DP, TPS, MODE>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  const int BH = p.B * p.H;
+  dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk);
+  const int threads = ((p.M + 63) & ~63) * nvec * TPS;
+  hipLaunchKernelGGL((seg_partial_kernel<T, DP, TPS, MODE>), grid, dim3(threads), lds, st, p, pp);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const int G = (p.M + GS - 1) / GS;
+  hipLaunchKernelGGL((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G), dim3(256), 0, st,
+                     p, pp);
+  return hipGetLastError();
+}
+
+template <typename T, int DP, int MODE>
+hipError_t launch_part_tps(const SegParams& p, const PartParams& pp, int nvec, int tps, size_t lds,
+                           hipStream_t st) {
+  if constexpr (DP == 32) {
+    return launch_part<T, 32, 1, MODE>(p, pp, nvec, lds, st);
+  } else {
+    if (tps == DP / 32) return launch_part<T, DP, DP / 32, MODE>(p, pp, nvec, lds, st);
+    return launch_part<T, DP, DP / 64, MODE>(p, pp, nvec, lds, st);
+  }
+}
+
+template <typename T, int DP>
+hipError_t launch_seg_t(const SegParams& p, int mode, const PartParams* pp, hipStream_t st) {
+  const int nvec = (mode == SEG_UPDATE && p.b_same_as_a) ? 1 : 2;
+  const int tps = part_tps(DP, p.M, nvec);
+  const size_t lds = part_lds_bytes<T, DP>(p.M, mode, nvec);
+  if (pp && pp->nchunk > 0 && tps > 0 && lds <= 160 * 1024) {
+    if (mode == SEG_UPDATE) return launch_part_tps<T, DP, SEG_UPDATE>(p, *pp, nvec, tps, lds, st);
+    return launch_part_tps<T, DP, SEG_ATTBWD>(p, *pp, nvec, tps, lds, st);
+  }
+  const int G = (p.M + GS - 1) / GS;
+  dim3 grid(XCDS * ((p.B * p.H + XCDS - 1) / XCDS) * G);
   if (mode == SEG_UPDATE)
-    hipLaunchKernelGGL((seg_update_kernel<T, DP>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((seg_update_kernel<T, DP>), grid, dim3(SEG_THREADS), 0, st, p);
   else
-    hipLaunchKernelGGL((seg_attbwd_kernel<T, DP>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((seg_attbwd_kernel<T, DP>), grid, dim3(SEG_THREADS), 0, st, p);
   return hipGetLastError();
 }
 
@@ -406,12 +851,28 @@ inline int grid1d(int64_t n, int tpb = 256) {
 
 }  // namespace
 
-hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, hipStream_t st) {
+int seg_chunks(int B, int H, int N, int M, int D) {
+  // token-chunk path: about 256 blocks of whole sub-chunks, at most NCMAX per (b,h)
+  const int DP = D <= 32 ? 32 : (D <= 64 ? 64 : 128);
+  if (part_tps(DP, M, 1) == 0) return 0;
+  const int BH = B * H;
+  const int per = (N + SUB - 1) / SUB;
+  int c = (256 + BH - 1) / BH;
+  if (c > NCMAX) c = NCMAX;
+  return c < 1 ? 1 : (c > per ? per : c);
+}
+
+int seg_chunk_tokens(int N, int nchunk) {
+  const int sub = (N + SUB - 1) / SUB;
+  return ((sub + nchunk - 1) / nchunk) * SUB;
+}
+
+hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp, hipStream_t st) {
 #define MURM_SEG(T)                                           \
   switch (DP) {                                               \
-    case 32: return launch_seg_t<T, 32>(p, mode, st);         \
-    case 64: return launch_seg_t<T, 64>(p, mode, st);         \
-    case 128: return launch_seg_t<T, 128>(p, mode, st);       \
+    case 32: return launch_seg_t<T, 32>(p, mode, pp, st);     \
+    case 64: return launch_seg_t<T, 64>(p, mode, pp, st);     \
+    case 128: return launch_seg_t<T, 128>(p, mode, pp, st);   \
     default: return hipErrorInvalidValue;                     \
   }
   switch (dtype) {
@@ -424,7 +885,7 @@ hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, hipStream
 }
 
 hipError_t launch_du(const DuParams& p, hipStream_t st) {
-  hipLaunchKernelGGL(du_kernel, dim3(p.B * p.H), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(du_kernel, dim3((p.M + 3) / 4, p.B * p.H), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 

@@ -205,6 +205,7 @@ class _SlotMurmurate(torch.autograd.Function):
         lib = _get_lib()
         out, indices, weights, ws = lib.slot_murmurate_fwd(
             q, x, tk, tv, slot_keys, slot_values, rounds, alpha, gamma, causal, effective_M, mask, scale)
+        ctx.set_materialize_grads(False)  # unused outputs need no zero-filled gradients
         ctx.save_for_backward(q, tk, tv, slot_keys, weights)
         ctx.ws = ws
         ctx.cfg = (rounds, alpha, gamma, scale, x is not None)

@@ -8,8 +8,9 @@ and records, as small .npz fixtures next to this script:
 
 * legacy_composite.npz -- ``slot_murmurate_reference`` (reference.py:138-192)
   on seeded fp32 inputs for several flag combinations (plain, causal, dynamic
-  M, token mask + position-bias callable, and x = q = k = v, which is the
-  README call form), and the config-1 shapes (B=2, H=4, N=128, d=64, M=256).
+  M, token mask + position-bias callable, partial mask + bias callable, and
+  x = q = k = v, which is the README call form), and the config-1 shapes
+  (B=2, H=4, N=128, d=64, M=256).
   The composition of the four phases (which tensor feeds which phase, residual
   placement, post-update diffusion neighbours) is what no closed form pins.
 * select_ties.npz -- ``slot_select_reference`` (reference.py:6-39) on inputs
@@ -78,6 +79,25 @@ def legacy_cases(ref):
     out = ref.slot_murmurate_reference(x, q, k, v, ske, sve, num_heads=H, rounds=R,
                                        mask=mask, position_bias_fn=bias_fn)
     p = "maskbias__"
+    cases.update({p + "x": _t(x), p + "q": _t(q), p + "k": _t(k), p + "v": _t(v),
+                  p + "ske": _t(ske), p + "sve": _t(sve), p + "mask": _t(mask),
+                  p + "out": _t(out)})
+    cases[p + "meta"] = np.array([B, N, H, Dh, M, R], dtype=np.int64)
+
+    # partial [B,H,N,M] mask (every token keeps >= 7 slots, so no -inf ties)
+    # plus the same bias callable: comparable on a device whose tie order
+    # differs from torch.topk's
+    B, N, H, Dh, M, R = 2, 24, 2, 16, 32, 3
+    D = H * Dh
+    x, q, k, v = rn(B, N, D), rn(B, N, D), rn(B, N, D), rn(B, N, D)
+    ske, sve = rn(H, M, Dh), rn(H, M, Dh, std=0.5)
+    gm = torch.Generator().manual_seed(3)
+    mask = (torch.rand(B, H, N, M, generator=gm) > 0.4).float()
+    mask[..., :8] = 1.0
+    ramp = torch.linspace(-1.0, 1.0, M)
+    out = ref.slot_murmurate_reference(x, q, k, v, ske, sve, num_heads=H, rounds=R,
+                                       mask=mask, position_bias_fn=bias_fn)
+    p = "maskpart__"
     cases.update({p + "x": _t(x), p + "q": _t(q), p + "k": _t(k), p + "v": _t(v),
                   p + "ske": _t(ske), p + "sve": _t(sve), p + "mask": _t(mask),
                   p + "out": _t(out)})

@@ -44,13 +44,17 @@ def seeded(shape_list, seed=42, stds=None):
     return out
 
 
-def assert_close(name, got, ref, dtype, mask=None):
+def assert_close(name, got, ref, dtype, mask=None, extra=None):
+    """|got - ref| <= atol + rtol*|ref| (+ extra, a per-element bound where the
+    quantity is ill-conditioned in float32)."""
     atol, rtol = TOL[dtype]
     g = got.detach().double().cpu()
     r = ref.detach().double().cpu()
     assert g.shape == r.shape, (name, g.shape, r.shape)
     diff = (g - r).abs()
     tol = atol + rtol * r.abs()
+    if extra is not None:
+        tol = tol + extra.double().cpu()
     bad = diff > tol
     if mask is not None:
         bad = bad & mask
@@ -77,6 +81,27 @@ def check_selection(name, gpu_idx, scores, k=7):
     assert int(gi.min()) >= 0 and int(gi.max()) < M, f"{name}: index out of range"
     assert (gi.sort(-1).values.diff(dim=-1) > 0).all(), f"{name}: repeated index"
     return float(set_ok.double().mean())
+
+
+def grad_w_bound(tk, tv, gk, gv, idx, w, alpha, eps=1e-8):
+    """Float32 error bound of the update's weight gradient.
+
+    dw_nj = (1-a)/(W_m+eps) [(tk_n - K_m/(W_m+eps)).G'k_m + (tv_n - V_m/(W_m+eps)).G'v_m],
+    m = idx_nj: the two halves cancel on slots whose total weight W_m is small,
+    so any float32 evaluation (the reference's included) carries an error of
+    about D * 2^-24 * (1-a)/W_m * (|tk|+|mean|).|G'| -- bounded here with
+    2^-17 per term (D <= 128)."""
+    M = gk.shape[2]
+    tk, tv, gk, gv = (t.double() for t in (tk, tv, gk, gv))
+    K, V, W = O.slot_sums(tk, tv, idx, w.double(), M)
+    mk, mv = K / (W.unsqueeze(-1) + eps), V / (W.unsqueeze(-1) + eps)
+    B, H, N, _ = tk.shape
+    b = torch.arange(B).view(B, 1, 1, 1)
+    h = torch.arange(H).view(1, H, 1, 1)
+    ag = lambda t: t.abs()[b, h, idx]  # noqa: E731
+    mag = ((tk.abs().unsqueeze(3) + ag(mk)) * ag(gk)).sum(-1) + ((tv.abs().unsqueeze(3) + ag(mv)) * ag(gv)).sum(-1)
+    cond = (1.0 - alpha) / (W[b, h, idx] + eps) * mag
+    return cond * 2.0 ** -17
 
 
 def round_indices(ws, B, H, N, D, M, R, shared, r):

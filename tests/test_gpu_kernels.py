@@ -14,7 +14,7 @@ import torch
 import murmurative as MA
 from murmurative import capi
 from oracle import murm_oracle as O
-from parity import TOL, assert_close, check_selection, seeded
+from parity import TOL, assert_close, check_selection, grad_w_bound, seeded
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -140,15 +140,23 @@ def test_zero_scores_keep_distinct_indices():
     assert torch.allclose(w.cpu(), torch.full_like(w.cpu(), 1 / 7))
 
 
-UPD_CASES = [(1, 2, 40, 16, 64), (2, 2, 300, 64, 256), (1, 1, 1500, 128, 48), (1, 2, 64, 32, 3 + 4)]
+# (B, H, N, D, M, duplicates): the token-chunk reduction serves M padded to 64
+# times the per-slot threads up to 1024; (1, 2, 500, 96, 520) takes the
+# per-slot-group kernels instead.  With duplicates a token names a slot twice
+# (caller-given indices; the reference's index_add counts both).
+UPD_CASES = [(1, 2, 40, 16, 64, 0), (2, 2, 300, 64, 256, 0), (1, 1, 1500, 128, 48, 0), (1, 2, 64, 32, 3 + 4, 0),
+             (1, 2, 500, 96, 520, 0), (1, 2, 700, 64, 32, 1)]
 
 
-def _update_inputs(B, H, N, D, M, dtype, seed=5):
+def _update_inputs(B, H, N, D, M, dtype, seed=5, dup=False):
     tk, tv, sk, sv, gk, gv = seeded([(B, H, N, D), (B, H, N, D), (B, H, M, D), (B, H, M, D), (B, H, M, D),
                                      (B, H, M, D)], seed)
     g = torch.Generator().manual_seed(seed)
     used = M - 3 if M > 10 else M  # with M > 10 the last three slots stay unused (W = 0)
-    idx = torch.stack([torch.randperm(used, generator=g)[:7] for _ in range(B * H * N)]).view(B, H, N, 7)
+    if dup:
+        idx = torch.randint(0, used, (B, H, N, 7), generator=g)
+    else:
+        idx = torch.stack([torch.randperm(used, generator=g)[:7] for _ in range(B * H * N)]).view(B, H, N, 7)
     w = torch.rand(B, H, N, 7, generator=g)
     w = w / w.sum(-1, keepdim=True)
     cast = lambda t: t.to(dtype)  # noqa: E731
@@ -158,9 +166,9 @@ def _update_inputs(B, H, N, D, M, dtype, seed=5):
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "f16", "bf16"])
 @pytest.mark.parametrize("case", UPD_CASES, ids=[f"u{i}" for i in range(len(UPD_CASES))])
 def test_update_and_diffusion_ops(dtype, case):
-    B, H, N, D, M = case
+    B, H, N, D, M, dup = case
     _print_case("update/diffusion", dtype, case)
-    tk, tv, sk, sv, gk, gv, idx, w = _update_inputs(B, H, N, D, M, dtype)
+    tk, tv, sk, sv, gk, gv, idx, w = _update_inputs(B, H, N, D, M, dtype, dup=bool(dup))
     a, gm = 0.8, 0.15
     # forward, in place
     skd, svd = sk.to(DEV).clone(), sv.to(DEV).clone()
@@ -180,21 +188,35 @@ def test_update_and_diffusion_ops(dtype, case):
     h_k, h_v = O.diffusion(e_k, e_v, gm)  # post-update neighbours
     assert_close("update_diffuse k", skd3, h_k, dtype)
     assert_close("update_diffuse v", svd3, h_v, dtype)
-    # backward of the update and of update+diffuse through autograd
+    # update backward op, given the gradient it receives (ops.py:117-130)
+    gtk, gtv, gok, gov, gw_ = lib.slot_update_backward(gk.to(DEV), gv.to(DEV), tk.to(DEV), tv.to(DEV),
+                                                       idx.to(DEV), w.to(DEV), a)
+    tk64, tv64, sk64, sv64 = (t.double().requires_grad_(True) for t in (tk, tv, sk, sv))
+    w64 = w.double().requires_grad_(True)
+    ok_, ov_ = O.update(tk64, tv64, sk64, sv64, idx, w64, a)
+    ((ok_ * gk.double()).sum() + (ov_ * gv.double()).sum()).backward()
+    assert_close("update bwd token keys", gtk, tk64.grad, dtype)
+    assert_close("update bwd token values", gtv, tv64.grad, dtype)
+    assert_close("update bwd slot keys", gok, sk64.grad, dtype)
+    assert_close("update bwd slot values", gov, sv64.grad, dtype)
+    assert_close("update bwd weights", gw_, w64.grad, dtype, extra=grad_w_bound(tk, tv, gk, gv, idx, w, a))
+    # update + diffusion through autograd: the adjoint crosses the op boundary
+    # in the slot dtype (ops.py:188-208), so the oracle rounds it there too
     tkd, tvd, skg, svg = (t.to(DEV).requires_grad_(True) for t in (tk, tv, sk, sv))
     wd = w.to(DEV).requires_grad_(True)
     nk, nv = MA.ops._SlotUpdateDiffuse.apply(tkd, tvd, skg.clone(), svg.clone(), idx.to(DEV), wd, a, gm)
     (nk.float() * gk.to(DEV).float()).sum().add((nv.float() * gv.to(DEV).float()).sum()).backward()
+    gpk = O.diffusion_transpose(gk.double(), gm).to(dtype)
+    gpv = O.diffusion_transpose(gv.double(), gm).to(dtype)
     tk64, tv64, sk64, sv64 = (t.double().requires_grad_(True) for t in (tk, tv, sk, sv))
     w64 = w.double().requires_grad_(True)
     ok_, ov_ = O.update(tk64, tv64, sk64, sv64, idx, w64, a)
-    dk_, dv_ = O.diffusion(ok_, ov_, gm)
-    ((dk_ * gk.double()).sum() + (dv_ * gv.double()).sum()).backward()
-    assert_close("bwd token keys", tkd.grad, tk64.grad, dtype)
-    assert_close("bwd token values", tvd.grad, tv64.grad, dtype)
-    assert_close("bwd slot keys", skg.grad, sk64.grad, dtype)
-    assert_close("bwd slot values", svg.grad, sv64.grad, dtype)
-    assert_close("bwd weights", wd.grad, w64.grad, torch.float32 if dtype == torch.float32 else dtype)
+    ((ok_ * gpk.double()).sum() + (ov_ * gpv.double()).sum()).backward()
+    assert_close("chain bwd token keys", tkd.grad, tk64.grad, dtype)
+    assert_close("chain bwd token values", tvd.grad, tv64.grad, dtype)
+    assert_close("chain bwd slot keys", skg.grad, sk64.grad, dtype)
+    assert_close("chain bwd slot values", svg.grad, sv64.grad, dtype)
+    assert_close("chain bwd weights", wd.grad, w64.grad, dtype, extra=grad_w_bound(tk, tv, gpk, gpv, idx, w, a))
     # diffusion backward op alone
     gdk, gdv = lib.slot_diffusion_backward(gk.to(DEV), gv.to(DEV), gm)
     assert_close("diffusion adjoint k", gdk, O.diffusion_transpose(gk.double(), gm), dtype)

@@ -242,6 +242,18 @@ def test_legacy_composite_golden_mask_and_bias():
     assert torch.allclose(out[fin], t["out"][fin], atol=2e-5, rtol=1e-5)
 
 
+def test_legacy_composite_golden_partial_mask_and_bias():
+    d = np.load(os.path.join(GOLD, "legacy_composite.npz"))
+    B, N, H, Dh, M, R = [int(v) for v in d["maskpart__meta"]]
+    t = {k: torch.from_numpy(d[f"maskpart__{k}"]) for k in
+         ("x", "q", "k", "v", "ske", "sve", "mask", "out")}
+    ramp = torch.linspace(-1.0, 1.0, M)
+    out = O.murmurate_legacy(t["x"], t["q"], t["k"], t["v"], t["ske"], t["sve"], num_heads=H,
+                             rounds=R, mask=t["mask"],
+                             position_bias_fn=lambda xh: 0.25 * torch.tanh(xh[..., :1]) * ramp)
+    assert torch.allclose(out, t["out"], atol=2e-5, rtol=1e-5)
+
+
 def test_readme_form_golden_config1():
     d = np.load(os.path.join(GOLD, "legacy_composite.npz"))
     B, N, H, Dh, M, R = [int(v) for v in d["readme_cfg1__meta"]]
