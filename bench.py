@@ -52,10 +52,17 @@ def byte_model(B, H, N, D, M, R, e):
         "select_attend": (R * (tok + S + idx + w) + T * 56) / R,
         # q, R rounds of (indices, weights, value table) in; out written
         "gather_out": tok + R * (idx + w + S) + tok,
-        # q, indices, weights, 2 old slot tables in; 2 new tables, key sums, weight sums out
-        "seg_update": tok + idx + w + 2 * S + 2 * S + S + Wb,
-        # q, grad_out, ds, weights, indices, 2 carries in; 2 slot grads out
-        "seg_attbwd": 2 * tok + w + w + idx + 2 * S + 2 * S,
+        # token-chunk partial sums of the update: q, indices, weights in (the
+        # partials themselves are scratch, not algorithmic traffic)
+        "seg_update": tok + idx + w,
+        # chunk reduction + EMA + diffusion: 2 old slot tables in; 2 new tables,
+        # key sums, weight sums out
+        "seg_update_reduce": 2 * S + 2 * S + S + Wb,
+        # partial sums of the slot-side attend backward: q, grad_out, ds, weights, indices in
+        "seg_attbwd": 2 * tok + w + w + idx,
+        # reduction + carry + previous round's diffusion adjoint / EMA backward:
+        # 2 carries, key sums, weight sums in; dK, 2 carries, dW out
+        "seg_attbwd_reduce": 2 * S + S + Wb + 3 * S + Wb,
         # 2 grads, key sums, weight sums in; dK, 2 carries, dW out
         "du": 2 * S + S + Wb + 3 * S + Wb,
         # grad_out, q, indices, weights, value table, dK, dW in; ds out (external grad_w once)
@@ -67,6 +74,23 @@ def byte_model(B, H, N, D, M, R, e):
     }
     flops = {"select_attend": 2.0 * T * M * D}
     return per_launch, flops
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "slot_murmurate_fwd_bwd_headline_hbm_traffic.md")
+
+
+def measured_traffic(config):
+    """HBM bytes per launch of each timing class, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary of the headline run (copy-kernel calibrated);
+    {} for other configs or when the summary is absent."""
+    if config != "3" or not os.path.exists(TRAFFIC_FILE):
+        return {}
+    out = {}
+    for line in open(TRAFFIC_FILE):
+        if line.startswith("traffic: "):
+            _, cls, val = line.split()
+            out[cls] = int(val)
+    return out
 
 
 def make_inputs(cfg, device, seed=42):
@@ -118,6 +142,9 @@ def main():
     ap.add_argument("--config", default="3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after the timed passes, copy a MIB-MiB tensor 3 times (a plain copy kernel of known "
+                         "size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {a.gpus}); the kernels run per (b,h) "
@@ -172,9 +199,12 @@ def main():
                          "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     dom = max(kt, key=lambda k: kt[k][0])
     dk = kernels[dom]
+    traffic = measured_traffic(a.config)
     roofline = {"kernel": dom, "bound": "hbm", "achieved": dk["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dk["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(dk["GB_s"] / HBM_PEAK_GBS, 4), "traffic": traffic.get(dom),
                 "bytes_per_launch": int(per_launch[dom]), "avg_us": dk["avg_us"]}
+    if traffic.get(dom) is not None:
+        roofline["traffic_source"] = os.path.relpath(TRAFFIC_FILE, ROOT)
     if "select_attend" in kt:
         sa_ms, sa_n = kt["select_attend"]
         tf = flops["select_attend"] / (sa_ms / sa_n * 1e-3) / 1e12
@@ -194,6 +224,16 @@ def main():
         "kernels": kernels,
         "device_ms_per_step_in_kernels": round(device_ms, 4),
     }
+    if a.copy_calibration > 0:
+        n = a.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        res["copy_calibration_bytes_each_way"] = n * 4
+        del src, dst
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(cfg, a.cpu_budget)
     print(json.dumps(res), flush=True)

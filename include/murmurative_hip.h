@@ -254,9 +254,11 @@ int murm_murmurate_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
  * kernel launch is bracketed by HIP events on its stream; murm_timing_read
  * waits for the recorded events and returns the summed device time (ms) and
  * launch count of one kernel class.  Classes: 0 select_attend, 1 gather_out,
- * 2 seg_update, 3 seg_attbwd, 4 du, 5 tok_bwd, 6 tok_grad, 7 conversions.
+ * 2 seg_update, 3 seg_attbwd, 4 du, 5 tok_bwd, 6 tok_grad, 7 conversions,
+ * 8 seg_update_reduce, 9 seg_attbwd_reduce (2 and 3 are the partial-sum
+ * kernels when 8 and 9 run, else the whole reduction).
  * ------------------------------------------------------------------------- */
-#define MURM_TIMING_CLASSES 8
+#define MURM_TIMING_CLASSES 10
 void murm_timing_enable(int on);
 void murm_timing_reset(void);
 int murm_timing_read(int cls, double* total_ms, int64_t* launches);

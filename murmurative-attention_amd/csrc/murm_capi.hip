@@ -33,8 +33,9 @@ int fail(int code, const char* fmt, ...) {
 
 // ------------------------------------------------------------- timing ---
 const char* kClassNames[MURM_TIMING_CLASSES] = {"select_attend", "gather_out", "seg_update", "seg_attbwd",
-                                                "du", "tok_bwd", "tok_grad", "conversions"};
-enum Cls { C_SA = 0, C_OUT, C_SEGU, C_SEGB, C_DU, C_TOKB, C_TOKG, C_CONV };
+                                                "du", "tok_bwd", "tok_grad", "conversions",
+                                                "seg_update_reduce", "seg_attbwd_reduce"};
+enum Cls { C_SA = 0, C_OUT, C_SEGU, C_SEGB, C_DU, C_TOKB, C_TOKG, C_CONV, C_SEGUR, C_SEGBR };
 
 struct Timing {
   std::mutex mu;
@@ -473,7 +474,9 @@ int murm_select_attend_bwd(int dtype, int slot_dtype, int B, int H, int N, int D
   SegParams s = seg_base(B, H, N, D, M);
   s.idx = L.idx; s.wgt = weights; s.ds = L.ds; s.ds_scale = c; s.va = qv; s.vb = g;
   s.final_out = 1; s.gk_out = L.dk; s.gv_out = L.dv;
-  RUN(C_SEGB, "seg_attbwd", launch_seg(dtype, DP, SEG_ATTBWD, s, &L.part, st));
+  RUN(C_SEGB, "seg_attbwd", launch_seg(dtype, DP, SEG_ATTBWD, s, &L.part, 0, st));
+  if (seg_two_stage(dtype, DP, SEG_ATTBWD, s, &L.part))
+    RUN(C_SEGBR, "seg_attbwd_reduce", launch_seg(dtype, DP, SEG_ATTBWD, s, &L.part, 1, st));
   const int64_t ssb = (int64_t)H * M * D, ssh = (int64_t)M * D, ssm = D;
   RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.dk, grad_sk, ssb, ssh, ssm, B, H, M, D, st));
   RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.dv, grad_sv, ssb, ssh, ssm, B, H, M, D, st));
@@ -515,7 +518,9 @@ static int update_common(int dtype, int slot_dtype, int B, int H, int N, int D, 
   s.b_same_as_a = 0;
   s.sk_old = L.sk; s.sv_old = L.sv; s.sk_new = L.nk; s.sv_new = L.nv;
   s.alpha = (float)alpha; s.gamma = (float)gamma; s.diffuse = diffuse;
-  RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, st));
+  RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, 0, st));
+  if (seg_two_stage(dtype, DP, SEG_UPDATE, s, &L.part))
+    RUN(C_SEGUR, "seg_update_reduce", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, 1, st));
   RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.nk, sk, sk_sb, sk_sh, sk_sm, B, H, M, D, st));
   RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.nv, sv, sv_sb, sv_sh, sv_sm, B, H, M, D, st));
   return MURM_OK;
@@ -571,7 +576,9 @@ int murm_slot_update_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, 
   SegParams s = seg_base(B, H, N, D, M);
   s.idx = L.idx; s.wgt = weights; s.va = tkv; s.vb = tvv; s.b_same_as_a = 0;
   s.ksum = L.K; s.vsum = L.V; s.wsum = L.W;
-  RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, st));
+  RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, 0, st));
+  if (seg_two_stage(dtype, DP, SEG_UPDATE, s, &L.part))
+    RUN(C_SEGUR, "seg_update_reduce", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, 1, st));
   DuParams d{};
   d.B = B; d.H = H; d.M = M; d.D = D;
   d.Gk = L.sk; d.Gv = L.sv; d.K = L.K; d.V = L.V; d.W = L.W;
@@ -672,7 +679,9 @@ int murm_murmurate_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
     s.sk_old = L.sk[r]; s.sv_old = L.sv[r]; s.sk_new = L.sk[r + 1]; s.sv_new = L.sv[r + 1];
     s.ksum = L.ksum[r]; s.vsum = shared ? nullptr : L.vsum[r]; s.wsum = L.wsum[r];
     s.alpha = (float)alpha; s.gamma = (float)gamma; s.diffuse = 1;
-    RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, st));
+    RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, 0, st));
+    if (seg_two_stage(dtype, DP, SEG_UPDATE, s, &L.part))
+      RUN(C_SEGUR, "seg_update_reduce", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, 1, st));
   }
   OutParams o{};
   o.base = x ? tv_of(x, x_sb, x_sh, x_sn, dtype) : qv;
@@ -770,7 +779,9 @@ int murm_murmurate_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
       s.final_out = 1;
       s.gk_out = G.Gk; s.gv_out = G.Gv;
     }
-    RUN(C_SEGB, "seg_attbwd", launch_seg(dtype, DP, SEG_ATTBWD, s, &G.part, st));
+    RUN(C_SEGB, "seg_attbwd", launch_seg(dtype, DP, SEG_ATTBWD, s, &G.part, 0, st));
+    if (seg_two_stage(dtype, DP, SEG_ATTBWD, s, &G.part))
+      RUN(C_SEGBR, "seg_attbwd_reduce", launch_seg(dtype, DP, SEG_ATTBWD, s, &G.part, 1, st));
     if (r == 0) {
       const int64_t ssb = (int64_t)H * M * D, ssh = (int64_t)M * D, ssm = D;
       RUN(C_CONV, "from_state", launch_from_state(slot_dtype, G.Gk, grad_sk, ssb, ssh, ssm, B, H, M, D, st));

@@ -118,7 +118,11 @@ hipError_t launch_select_attend(int dtype, int DP, const SAParams& p, hipStream_
 hipError_t launch_gather_out(int dtype, int DP, const OutParams& p, hipStream_t st);
 int seg_chunks(int B, int H, int N, int M, int D);   // 0: no token-chunk path for this shape
 int seg_chunk_tokens(int N, int nchunk);
-hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp, hipStream_t st);
+// stage 0: partial sums (token-chunk path) or the whole reduction (pull kernels);
+// stage 1: chunk reduction + epilogue, only when seg_two_stage() is true.
+bool seg_two_stage(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp);
+hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp, int stage,
+                      hipStream_t st);
 hipError_t launch_du(const DuParams& p, hipStream_t st);
 hipError_t launch_tok_bwd(int dtype, int DP, const TokBwdParams& p, hipStream_t st);
 hipError_t launch_tok_grad(int dtype, int DP, const TokGradParams& p, hipStream_t st);

@@ -122,17 +122,44 @@ __global__ __launch_bounds__(256) void sa_kernel16(SAParams p) {
   const int b = bh / p.H, h = bh % p.H;
   const float* skb = p.sk + (int64_t)bh * p.M * p.D;
 
-  for (int i = threadIdx.x; i < Mp * (DP / 4); i += blockDim.x) {
-    const int m = i / (DP / 4), d4 = (i % (DP / 4)) * 4;
-    float v[4];
+  // stage the keys: batches of STB float4 loads in flight per thread, then
+  // the hi/lo split written as 8-byte LDS stores
+  constexpr int STB = 8;
+  const int nq = Mp * (DP / 4);
+  const bool vec4 = (p.D & 3) == 0;
+  for (int i0 = threadIdx.x; i0 < nq; i0 += STB * blockDim.x) {
+    float4 v[STB];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = (m < p.M && d4 + e < p.D) ? skb[(int64_t)m * p.D + d4 + e] : 0.f;
+    for (int u = 0; u < STB; ++u) {
+      const int i = i0 + u * blockDim.x;
+      const int m = i / (DP / 4), d4 = (i % (DP / 4)) * 4;
+      v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < nq && m < p.M && d4 < p.D) {
+        const float* src = skb + (int64_t)m * p.D + d4;
+        if (vec4) {
+          v[u] = *reinterpret_cast<const float4*>(src);
+        } else {
+          v[u].x = src[0];
+          v[u].y = d4 + 1 < p.D ? src[1] : 0.f;
+          v[u].z = d4 + 2 < p.D ? src[2] : 0.f;
+          v[u].w = d4 + 3 < p.D ? src[3] : 0.f;
+        }
+      }
+    }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const T hi = (T)v[e];
-      const T lo = (T)(v[e] - (float)hi);
-      lhi[m * ROW + d4 + e] = hi;
-      llo[m * ROW + d4 + e] = lo;
+    for (int u = 0; u < STB; ++u) {
+      const int i = i0 + u * blockDim.x;
+      if (i >= nq) break;
+      const int m = i / (DP / 4), d4 = (i % (DP / 4)) * 4;
+      const float f[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      T hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hi[e] = (T)f[e];
+        lo[e] = (T)(f[e] - (float)hi[e]);
+      }
+      *reinterpret_cast<uint2*>(lhi + m * ROW + d4) = *reinterpret_cast<const uint2*>(hi);
+      *reinterpret_cast<uint2*>(llo + m * ROW + d4) = *reinterpret_cast<const uint2*>(lo);
     }
   }
   __syncthreads();
@@ -256,9 +283,35 @@ __global__ __launch_bounds__(256) void sa_kernel32(SAParams p) {
   const int bh = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
   const float* skb = p.sk + (int64_t)bh * p.M * p.D;
-  for (int i = threadIdx.x; i < Mp * DP; i += blockDim.x) {
-    const int m = i / DP, d = i % DP;
-    lsk[m * ROW + d] = (m < p.M && d < p.D) ? skb[(int64_t)m * p.D + d] : 0.f;
+  constexpr int STB = 8;
+  const int nq = Mp * (DP / 4);
+  const bool vec4 = (p.D & 3) == 0;
+  for (int i0 = threadIdx.x; i0 < nq; i0 += STB * blockDim.x) {
+    float4 v[STB];
+#pragma unroll
+    for (int u = 0; u < STB; ++u) {
+      const int i = i0 + u * blockDim.x;
+      const int m = i / (DP / 4), d4 = (i % (DP / 4)) * 4;
+      v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < nq && m < p.M && d4 < p.D) {
+        const float* src = skb + (int64_t)m * p.D + d4;
+        if (vec4) {
+          v[u] = *reinterpret_cast<const float4*>(src);
+        } else {
+          v[u].x = src[0];
+          v[u].y = d4 + 1 < p.D ? src[1] : 0.f;
+          v[u].z = d4 + 2 < p.D ? src[2] : 0.f;
+          v[u].w = d4 + 3 < p.D ? src[3] : 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < STB; ++u) {
+      const int i = i0 + u * blockDim.x;
+      if (i >= nq) break;
+      const int m = i / (DP / 4), d4 = (i % (DP / 4)) * 4;
+      *reinterpret_cast<float4*>(lsk + m * ROW + d4) = v[u];
+    }
   }
   __syncthreads();
 

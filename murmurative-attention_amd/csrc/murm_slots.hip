@@ -800,41 +800,53 @@ size_t part_lds_bytes(int M, int mode, int nvec) {
 }
 
 template <typename T, int DP, int TPS, int MODE>
-hipError_t launch_part(const SegParams& p, const PartParams& pp, int nvec, size_t lds, hipStream_t st) {
-  const void* fn = reinterpret_cast<const void*>(&seg_partial_kernel<T, DP, TPS, MODE>);
-  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return e;
+hipError_t launch_part(const SegParams& p, const PartParams& pp, int nvec, size_t lds, int stage, hipStream_t st) {
   const int BH = p.B * p.H;
-  dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk);
-  const int threads = ((p.M + 63) & ~63) * nvec * TPS;
-  hipLaunchKernelGGL((seg_partial_kernel<T, DP, TPS, MODE>), grid, dim3(threads), lds, st, p, pp);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  const int G = (p.M + GS - 1) / GS;
-  hipLaunchKernelGGL((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G), dim3(256), 0, st,
-                     p, pp);
+  if (stage == 0) {
+    const void* fn = reinterpret_cast<const void*>(&seg_partial_kernel<T, DP, TPS, MODE>);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk);
+    const int threads = ((p.M + 63) & ~63) * nvec * TPS;
+    hipLaunchKernelGGL((seg_partial_kernel<T, DP, TPS, MODE>), grid, dim3(threads), lds, st, p, pp);
+  } else {
+    const int G = (p.M + GS - 1) / GS;
+    hipLaunchKernelGGL((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G), dim3(256), 0,
+                       st, p, pp);
+  }
   return hipGetLastError();
 }
 
 template <typename T, int DP, int MODE>
-hipError_t launch_part_tps(const SegParams& p, const PartParams& pp, int nvec, int tps, size_t lds,
+hipError_t launch_part_tps(const SegParams& p, const PartParams& pp, int nvec, int tps, size_t lds, int stage,
                            hipStream_t st) {
   if constexpr (DP == 32) {
-    return launch_part<T, 32, 1, MODE>(p, pp, nvec, lds, st);
+    return launch_part<T, 32, 1, MODE>(p, pp, nvec, lds, stage, st);
   } else {
-    if (tps == DP / 32) return launch_part<T, DP, DP / 32, MODE>(p, pp, nvec, lds, st);
-    return launch_part<T, DP, DP / 64, MODE>(p, pp, nvec, lds, st);
+    if (tps == DP / 32) return launch_part<T, DP, DP / 32, MODE>(p, pp, nvec, lds, stage, st);
+    return launch_part<T, DP, DP / 64, MODE>(p, pp, nvec, lds, stage, st);
   }
 }
 
 template <typename T, int DP>
-hipError_t launch_seg_t(const SegParams& p, int mode, const PartParams* pp, hipStream_t st) {
-  const int nvec = (mode == SEG_UPDATE && p.b_same_as_a) ? 1 : 2;
-  const int tps = part_tps(DP, p.M, nvec);
-  const size_t lds = part_lds_bytes<T, DP>(p.M, mode, nvec);
-  if (pp && pp->nchunk > 0 && tps > 0 && lds <= 160 * 1024) {
-    if (mode == SEG_UPDATE) return launch_part_tps<T, DP, SEG_UPDATE>(p, *pp, nvec, tps, lds, st);
-    return launch_part_tps<T, DP, SEG_ATTBWD>(p, *pp, nvec, tps, lds, st);
+bool part_ok(const SegParams& p, int mode, const PartParams* pp, int& nvec, int& tps, size_t& lds) {
+  nvec = (mode == SEG_UPDATE && p.b_same_as_a) ? 1 : 2;
+  tps = part_tps(DP, p.M, nvec);
+  lds = part_lds_bytes<T, DP>(p.M, mode, nvec);
+  return pp && pp->nchunk > 0 && tps > 0 && lds <= 160 * 1024;
+}
+
+// stage 0: the partial-sum kernel (token-chunk path) or the whole pull kernel;
+// stage 1: the chunk reduction with the epilogue (token-chunk path only).
+template <typename T, int DP>
+hipError_t launch_seg_t(const SegParams& p, int mode, const PartParams* pp, int stage, hipStream_t st) {
+  int nvec, tps;
+  size_t lds;
+  if (part_ok<T, DP>(p, mode, pp, nvec, tps, lds)) {
+    if (mode == SEG_UPDATE) return launch_part_tps<T, DP, SEG_UPDATE>(p, *pp, nvec, tps, lds, stage, st);
+    return launch_part_tps<T, DP, SEG_ATTBWD>(p, *pp, nvec, tps, lds, stage, st);
   }
+  if (stage != 0) return hipSuccess;
   const int G = (p.M + GS - 1) / GS;
   dim3 grid(XCDS * ((p.B * p.H + XCDS - 1) / XCDS) * G);
   if (mode == SEG_UPDATE)
@@ -850,6 +862,25 @@ inline int grid1d(int64_t n, int tpb = 256) {
 }
 
 }  // namespace
+
+bool seg_two_stage(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp) {
+  int nvec, tps;
+  size_t lds;
+#define MURM_SEGQ(T)                                                   \
+  switch (DP) {                                                        \
+    case 32: return part_ok<T, 32>(p, mode, pp, nvec, tps, lds);       \
+    case 64: return part_ok<T, 64>(p, mode, pp, nvec, tps, lds);       \
+    case 128: return part_ok<T, 128>(p, mode, pp, nvec, tps, lds);     \
+    default: return false;                                             \
+  }
+  switch (dtype) {
+    case DT_BF16: MURM_SEGQ(__bf16)
+    case DT_F16: MURM_SEGQ(_Float16)
+    case DT_F32: MURM_SEGQ(float)
+    default: return false;
+  }
+#undef MURM_SEGQ
+}
 
 int seg_chunks(int B, int H, int N, int M, int D) {
   // token-chunk path: about 256 blocks of whole sub-chunks, at most NCMAX per (b,h)
@@ -867,12 +898,13 @@ int seg_chunk_tokens(int N, int nchunk) {
   return ((sub + nchunk - 1) / nchunk) * SUB;
 }
 
-hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp, hipStream_t st) {
-#define MURM_SEG(T)                                           \
-  switch (DP) {                                               \
-    case 32: return launch_seg_t<T, 32>(p, mode, pp, st);     \
-    case 64: return launch_seg_t<T, 64>(p, mode, pp, st);     \
-    case 128: return launch_seg_t<T, 128>(p, mode, pp, st);   \
+hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp, int stage,
+                      hipStream_t st) {
+#define MURM_SEG(T)                                                  \
+  switch (DP) {                                                      \
+    case 32: return launch_seg_t<T, 32>(p, mode, pp, stage, st);     \
+    case 64: return launch_seg_t<T, 64>(p, mode, pp, stage, st);     \
+    case 128: return launch_seg_t<T, 128>(p, mode, pp, stage, st);   \
     default: return hipErrorInvalidValue;                     \
   }
   switch (dtype) {

@@ -13,7 +13,7 @@ from ._hip_kernels import LIB_PATH
 
 F32, F16, BF16 = 0, 1, 2
 OK, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
-TIMING_CLASSES = 8
+TIMING_CLASSES = 10
 
 _p, _i, _l, _d, _sz, _f = C.c_void_p, C.c_int, C.c_int64, C.c_double, C.c_size_t, C.c_float
 _geom = [_i, _i, _i, _i, _i, _i, _i]           # dtype, slot_dtype, B, H, N, D, M
