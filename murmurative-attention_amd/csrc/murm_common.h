@@ -95,6 +95,25 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 }
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// Sum over aligned groups of G lanes (G = 2, 4, 8, 16), every lane of a group
+// receiving the same total, with DPP lane moves (no LDS round trip):
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.  The
+// adds pair lanes as a xor-1/2/4/8 butterfly, so the result is bitwise the
+// same in every lane of the group.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "group of 1, 2, 4, 8 or 16 lanes");
+  if constexpr (G >= 2) v += dpp_mov<0xB1>(v);
+  if constexpr (G >= 4) v += dpp_mov<0x4E>(v);
+  if constexpr (G >= 8) v += dpp_mov<0x141>(v);
+  if constexpr (G >= 16) v += dpp_mov<0x140>(v);
+  return v;
+}
+
 // ---------------------------------------------------- packed top-k keys ---
 // A selection key is the float score with its low `bits` mantissa bits
 // replaced by the slot index.  Float max/med3 then carry the index with the
@@ -173,5 +192,62 @@ struct RoundPtrs {
   const float* b[MAX_ROUNDS];        // second gathered table (optional)
   const float* c[MAX_ROUNDS];        // per-(token, j) coefficient for table b (optional)
 };
+
+// ------------------------------------------------------ LDS slot tables ---
+// Token-side kernels that gather slot rows stage the float32 [M, D] table of
+// the (b,h) in LDS (row stride DP + 4 floats, zero past D), eight float4
+// loads in flight per thread.  Rows past M are not written.
+template <int DP>
+__device__ __forceinline__ void stage_table(float* __restrict__ dst, const float* __restrict__ src, int M, int D) {
+  constexpr int RSD = DP + 4;
+  constexpr int STB = 8;
+  const int nq = M * (DP / 4);
+  const bool vec4 = (D & 3) == 0;
+  for (int i0 = threadIdx.x; i0 < nq; i0 += STB * blockDim.x) {
+    float4 v[STB];
+#pragma unroll
+    for (int u = 0; u < STB; ++u) {
+      const int i = i0 + u * blockDim.x;
+      const int m = i / (DP / 4), d4 = (i % (DP / 4)) * 4;
+      v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < nq && d4 < D) {
+        const float* s = src + (int64_t)m * D + d4;
+        if (vec4) {
+          v[u] = *reinterpret_cast<const float4*>(s);
+        } else {
+          v[u].x = s[0];
+          v[u].y = d4 + 1 < D ? s[1] : 0.f;
+          v[u].z = d4 + 2 < D ? s[2] : 0.f;
+          v[u].w = d4 + 3 < D ? s[3] : 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < STB; ++u) {
+      const int i = i0 + u * blockDim.x;
+      if (i >= nq) break;
+      const int m = i / (DP / 4), d4 = (i % (DP / 4)) * 4;
+      *reinterpret_cast<float4*>(dst + m * RSD + d4) = v[u];
+    }
+  }
+}
+
+// 8 floats of a staged table row (16-byte aligned: d0 % 8 == 0)
+__device__ __forceinline__ void lds8(const float* __restrict__ row, int d0, float (&o)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(row + d0);
+  const float4 b = *reinterpret_cast<const float4*>(row + d0 + 4);
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+
+// Blocks of the token-side kernels that stage tables: (b,h) x chunk on a 1-D
+// grid, every block of one (b,h) on XCD bh % 8 (linear id % 8 = XCD).
+constexpr int TOK_XCDS = 8;
+__device__ __forceinline__ bool tok_block(int BH, int nchunk, int& bh, int& chunk) {
+  const int L = blockIdx.x, x = L % TOK_XCDS, k = L / TOK_XCDS;
+  bh = x + TOK_XCDS * (k / nchunk);
+  chunk = k % nchunk;
+  return bh < BH;
+}
 
 }  // namespace murm

@@ -430,6 +430,75 @@ __global__ __launch_bounds__(256) void gather_out_kernel(OutParams p) {
   store8<T>(tok_row_mut<T>(p.out, b, h, n), d0, p.D, p.out.vec, acc);
 }
 
+// Staged variant: one block per (b,h) and token chunk; each round's value
+// table is staged in LDS (row stride DP + 4) in turn and every thread keeps
+// the outputs of its GO_PASSES tokens in registers across the rounds.
+constexpr int GO_THREADS = 512;
+constexpr int GO_PASSES = 8;
+
+template <typename T, int DP>
+__global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p, int nchunk) {
+  constexpr int DCH = DP / 8, TPP = GO_THREADS / DCH, RSD = DP + 4;
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* tab = reinterpret_cast<float*>(smem);
+  int bh, chunk;
+  if (!tok_block(p.B * p.H, nchunk, bh, chunk)) return;
+  const int b = bh / p.H, h = bh % p.H;
+  const int dc = threadIdx.x % DCH, d0 = dc * 8;
+  const int c_beg = chunk * GO_PASSES * TPP;
+  float acc[GO_PASSES][8];
+#pragma unroll
+  for (int q = 0; q < GO_PASSES; ++q) {
+    const int n = c_beg + q * TPP + threadIdx.x / DCH;
+    if (p.base.p && n < p.N) {
+      load8<T>(tok_row<T>(p.base, b, h, n), d0, p.D, p.base.vec, acc[q]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[q][i] = 0.f;
+    }
+  }
+  for (int r = 0; r < p.R; ++r) {
+    if (r > 0) __syncthreads();
+    stage_table<DP>(tab, p.rp.a[r] + (int64_t)bh * p.M * p.D, p.M, p.D);
+    __syncthreads();
+    // index rows and weights of pass q+1 are requested before pass q's gathers
+    uint4 irn;
+    float wn[KN];
+    auto fetch = [&](int q, uint4& ir, float (&w)[KN]) {
+      const int n = min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1);
+      const int64_t row = (int64_t)bh * p.N + n;
+      ir = *reinterpret_cast<const uint4*>(p.rp.idx[r] + row * IDX_ROW);
+#pragma unroll
+      for (int j = 0; j < KN; ++j) w[j] = p.rp.w[r][row * KN + j];
+    };
+    fetch(0, irn, wn);
+#pragma unroll
+    for (int q = 0; q < GO_PASSES; ++q) {
+      const uint4 ir = irn;
+      float wc[KN];
+#pragma unroll
+      for (int j = 0; j < KN; ++j) wc[j] = wn[j];
+      if (q + 1 < GO_PASSES) fetch(q + 1, irn, wn);
+      const int n = c_beg + q * TPP + threadIdx.x / DCH;
+      if (n >= p.N) continue;
+      const uint32_t sl[KN] = {ir.x & 0xFFFF, ir.x >> 16, ir.y & 0xFFFF, ir.y >> 16,
+                               ir.z & 0xFFFF, ir.z >> 16, ir.w & 0xFFFF};
+#pragma unroll
+      for (int j = 0; j < KN; ++j) {
+        float v[8];
+        lds8(tab + sl[j] * RSD, d0, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[q][i] += wc[j] * v[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < GO_PASSES; ++q) {
+    const int n = c_beg + q * TPP + threadIdx.x / DCH;
+    if (n < p.N) store8<T>(tok_row_mut<T>(p.out, b, h, n), d0, p.D, p.out.vec, acc[q]);
+  }
+}
+
 template <typename T, int DP>
 hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
   const int Mp = (p.M + 15) & ~15;
@@ -454,6 +523,18 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
 
 template <typename T, int DP>
 hipError_t launch_out_t(const OutParams& p, hipStream_t st) {
+  const size_t lds = (size_t)p.M * (DP + 4) * 4;
+  if (lds <= 150 * 1024) {
+    constexpr int TPP = GO_THREADS / (DP / 8);
+    const int BH = p.B * p.H;
+    const int nchunk = (p.N + GO_PASSES * TPP - 1) / (GO_PASSES * TPP);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_out_lds_kernel<T, DP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
+    hipLaunchKernelGGL((gather_out_lds_kernel<T, DP>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
+    return hipGetLastError();
+  }
   constexpr int TPB = 256 / (DP / 8);
   dim3 grid((p.N + TPB - 1) / TPB, p.B * p.H);
   hipLaunchKernelGGL((gather_out_kernel<T, DP>), grid, dim3(256), 0, st, p);

@@ -74,9 +74,7 @@ __global__ __launch_bounds__(256) void tok_bwd_kernel(TokBwdParams p) {
     dw[j] = s;
   }
 #pragma unroll
-  for (int x = 1; x < DCH; x <<= 1)
-#pragma unroll
-    for (int j = 0; j < KN; ++j) dw[j] += shfl_xor_f(dw[j], x);
+  for (int j = 0; j < KN; ++j) dw[j] = group_sum<DCH>(dw[j]);
   if (!live || dc != 0) return;
 #pragma unroll
   for (int j = 0; j < KN; ++j) {
@@ -156,6 +154,218 @@ __global__ __launch_bounds__(256) void tok_grad_kernel(TokGradParams p) {
   if (p.dtv.p) store8<T>(tok_row_mut<T>(p.dtv, b, h, n), d0, p.D, p.dtv.vec, av);
 }
 
+// ---------------------------------------------------------------------------
+// Staged variants: one block per (b,h) and token chunk stages the round's
+// float32 slot tables in LDS (row stride DP + 4), so the per-token gathers of
+// seven slot rows are LDS reads instead of L2 traffic.  Used when the tables
+// fit (e.g. M = 256, d = 64: 64 KiB per table).
+// ---------------------------------------------------------------------------
+constexpr int TOKS_THREADS = 512;
+
+template <int DP>
+struct TokShape {
+  static constexpr int DCH = DP / 8;                   // lanes per token
+  static constexpr int TPP = TOKS_THREADS / DCH;       // tokens per pass
+  static constexpr int RSD = DP + 4;                   // staged row stride
+};
+
+template <typename T, int DP>
+__global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams p, int nchunk, int chunk_tokens) {
+  using S = TokShape<DP>;
+  constexpr int DCH = S::DCH, TPP = S::TPP, RSD = S::RSD;
+  extern __shared__ __align__(16) unsigned char smem[];
+  int bh, chunk;
+  if (!tok_block(p.B * p.H, nchunk, bh, chunk)) return;
+  const int b = bh / p.H, h = bh % p.H;
+  const bool has_g = p.sv != nullptr, has_k = p.dkk != nullptr, has_v = p.dkv != nullptr;
+  float* t = reinterpret_cast<float*>(smem);
+  float* tsv = t;
+  float* tdk = tsv + (has_g ? p.M * RSD : 0);
+  float* tdv = tdk + (has_k ? p.M * RSD : 0);
+  float* tdw = tdv + (has_v ? p.M * RSD : 0);
+  const int64_t tb = (int64_t)bh * p.M * p.D;
+  if (has_g) stage_table<DP>(tsv, p.sv + tb, p.M, p.D);
+  if (has_k) stage_table<DP>(tdk, p.dkk + tb, p.M, p.D);
+  if (has_v) stage_table<DP>(tdv, p.dkv + tb, p.M, p.D);
+  if (p.dW)
+    for (int i = threadIdx.x; i < p.M; i += blockDim.x) tdw[i] = p.dW[(int64_t)bh * p.M + i];
+  __syncthreads();
+  const int dc = threadIdx.x % DCH, d0 = dc * 8;
+  const int c_beg = chunk * chunk_tokens, c_end = min(p.N, c_beg + chunk_tokens);
+  // a pass's index row and token rows are requested during the previous pass
+  float gn[8], an[8], cn[8];
+  uint32_t sln[KN];
+  auto fetch = [&](int n0) {
+    const int n = min(n0 + (int)threadIdx.x / DCH, c_end - 1);
+    unpack_idx(p.idx + ((int64_t)bh * p.N + n) * IDX_ROW, sln);
+    if (has_g) load8<T>(tok_row<T>(p.g, b, h, n), d0, p.D, p.g.vec, gn);
+    if (has_k) load8<T>(tok_row<T>(p.tk, b, h, n), d0, p.D, p.tk.vec, an);
+    if (has_v) load8<T>(tok_row<T>(p.tv, b, h, n), d0, p.D, p.tv.vec, cn);
+  };
+  if (c_beg < c_end) fetch(c_beg);
+  for (int n0 = c_beg; n0 < c_end; n0 += TPP) {
+    const int n = n0 + threadIdx.x / DCH;
+    const bool live = n < c_end;
+    const int nn = live ? n : c_beg;
+    const int64_t row = (int64_t)bh * p.N + nn;
+    uint32_t sl[KN];
+    float g[8], a[8], c[8];
+#pragma unroll
+    for (int j = 0; j < KN; ++j) sl[j] = sln[j];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { g[i] = gn[i]; a[i] = an[i]; c[i] = cn[i]; }
+    if (n0 + TPP < c_end) fetch(n0 + TPP);
+    float dw[KN];
+#pragma unroll
+    for (int j = 0; j < KN; ++j) {
+      float s = 0.f, v[8];
+      if (has_g) {
+        lds8(tsv + sl[j] * RSD, d0, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += g[i] * v[i];
+      }
+      if (has_k) {
+        lds8(tdk + sl[j] * RSD, d0, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += a[i] * v[i];
+      }
+      if (has_v) {
+        lds8(tdv + sl[j] * RSD, d0, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += c[i] * v[i];
+      }
+      dw[j] = s;
+    }
+#pragma unroll
+    for (int j = 0; j < KN; ++j) dw[j] = group_sum<DCH>(dw[j]);
+    if (live && dc == 0) {
+#pragma unroll
+      for (int j = 0; j < KN; ++j) {
+        if (p.dW) dw[j] += tdw[sl[j]];
+        if (p.gw) dw[j] += p.gw[row * KN + j];
+      }
+      if (p.dw_out) {
+#pragma unroll
+        for (int j = 0; j < KN; ++j) p.dw_out[row * KN + j] = dw[j];
+      }
+      if (p.ds_out) {
+        const float* w = p.w + row * KN;
+        float wj[KN], dot = 0.f;
+#pragma unroll
+        for (int j = 0; j < KN; ++j) { wj[j] = w[j]; dot += wj[j] * dw[j]; }
+#pragma unroll
+        for (int j = 0; j < KN; ++j) p.ds_out[row * KN + j] = wj[j] * (dw[j] - dot);
+      }
+    }
+  }
+}
+
+// tok_grad with each round's tables staged in LDS in turn; a thread keeps the
+// gradients of its PASSES tokens in registers across the rounds.
+template <typename T, int DP, int PASSES, bool KV>
+__global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParams p, int nchunk) {
+  using S = TokShape<DP>;
+  constexpr int DCH = S::DCH, TPP = S::TPP, RSD = S::RSD;
+  extern __shared__ __align__(16) unsigned char smem[];
+  int bh, chunk;
+  if (!tok_block(p.B * p.H, nchunk, bh, chunk)) return;
+  const int b = bh / p.H, h = bh % p.H;
+  float* t0 = reinterpret_cast<float*>(smem);
+  const int64_t tb = (int64_t)bh * p.M * p.D;
+  const int dc = threadIdx.x % DCH, d0 = dc * 8;
+  const int c_beg = chunk * PASSES * TPP;
+  constexpr int PK = KV ? PASSES : 1;  // token-key / token-value gradients (legacy form only)
+  float aq[PASSES][8], ak[PK][8], av[PK][8];
+#pragma unroll
+  for (int q = 0; q < PASSES; ++q) {
+    const int n = c_beg + q * TPP + threadIdx.x / DCH;
+    if (p.g.p && n < p.N) {
+      load8<T>(tok_row<T>(p.g, b, h, n), d0, p.D, p.g.vec, aq[q]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) aq[q][i] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < PK; ++q)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { ak[q][i] = 0.f; av[q][i] = 0.f; }
+  for (int r = 0; r < p.R; ++r) {
+    const bool use_sk = p.ds[r] && p.dq.p;
+    float* tsk = t0;
+    float* tdk = tsk + (use_sk ? p.M * RSD : 0);
+    float* tdv = tdk + (p.dkk[r] ? p.M * RSD : 0);
+    if (r > 0) __syncthreads();  // the previous round's tables are no longer read
+    if (use_sk) stage_table<DP>(tsk, p.sk[r] + tb, p.M, p.D);
+    if (p.dkk[r]) stage_table<DP>(tdk, p.dkk[r] + tb, p.M, p.D);
+    if (p.dkv[r]) stage_table<DP>(tdv, p.dkv[r] + tb, p.M, p.D);
+    __syncthreads();
+    // index rows, weights and softmax grads of pass q+1 are requested before
+    // pass q's gathers
+    uint32_t sln[KN];
+    float wn[KN], dn[KN];
+    auto fetch = [&](int q) {
+      const int n = min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1);
+      const int64_t row = (int64_t)bh * p.N + n;
+      unpack_idx(p.idx[r] + row * IDX_ROW, sln);
+#pragma unroll
+      for (int j = 0; j < KN; ++j) {
+        wn[j] = p.w[r][row * KN + j];
+        dn[j] = use_sk ? p.ds[r][row * KN + j] : 0.f;
+      }
+    };
+    fetch(0);
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q) {
+      uint32_t sl[KN];
+      float wr[KN], dsr[KN];
+#pragma unroll
+      for (int j = 0; j < KN; ++j) { sl[j] = sln[j]; wr[j] = wn[j]; dsr[j] = dn[j]; }
+      if (q + 1 < PASSES) fetch(q + 1);
+      const int n = c_beg + q * TPP + threadIdx.x / DCH;
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int j = 0; j < KN; ++j) {
+        float v[8];
+        if (use_sk) {
+          const float cj = p.c * dsr[j];
+          lds8(tsk + sl[j] * RSD, d0, v);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) aq[q][i] += cj * v[i];
+        }
+        const float wj = wr[j];
+        if (p.dkk[r]) {
+          lds8(tdk + sl[j] * RSD, d0, v);
+          if constexpr (KV) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ak[q][i] += wj * v[i];
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) aq[q][i] += wj * v[i];
+          }
+        }
+        if constexpr (KV) {
+          if (p.dkv[r]) {
+            lds8(tdv + sl[j] * RSD, d0, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) av[q][i] += wj * v[i];
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < PASSES; ++q) {
+    const int n = c_beg + q * TPP + threadIdx.x / DCH;
+    if (n >= p.N) continue;
+    if (p.dq.p) store8<T>(tok_row_mut<T>(p.dq, b, h, n), d0, p.D, p.dq.vec, aq[q]);
+    if constexpr (KV) {
+      if (p.dtk.p) store8<T>(tok_row_mut<T>(p.dtk, b, h, n), d0, p.D, p.dtk.vec, ak[q]);
+      if (p.dtv.p) store8<T>(tok_row_mut<T>(p.dtv, b, h, n), d0, p.D, p.dtv.vec, av[q]);
+    }
+  }
+}
+
 // Softmax weights for given indices: w_j = softmax_j(c * q.sk[I_j])
 // (reference.py:42-68 with the indices supplied by the caller).
 template <typename T, int DP>
@@ -185,9 +395,7 @@ __global__ __launch_bounds__(256) void attend_idx_kernel(AttendIdxParams p) {
     for (int i = 0; i < 8; ++i) s[j] += q[i] * v[i];
   }
 #pragma unroll
-  for (int x = 1; x < DCH; x <<= 1)
-#pragma unroll
-    for (int j = 0; j < KN; ++j) s[j] += shfl_xor_f(s[j], x);
+  for (int j = 0; j < KN; ++j) s[j] = group_sum<DCH>(s[j]);
   if (!live || dc != 0) return;
   float zmax = -INFINITY;
 #pragma unroll
@@ -208,16 +416,68 @@ hipError_t launch_attend_idx_t(const AttendIdxParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+// staged tables fit one block's LDS (leave room for a second block's worth of nothing)
+inline bool tables_fit(int nt, int M, int DP) {
+  return (size_t)nt * M * (DP + 4) * 4 + (size_t)M * 4 <= 150 * 1024;
+}
+
+// chunks per (b,h): about 256 blocks, whole passes per chunk
+inline int tok_chunks(int BH, int N, int tpp) {
+  const int passes = (N + tpp - 1) / tpp;
+  int c = (256 + BH - 1) / BH;
+  return c > passes ? passes : (c < 1 ? 1 : c);
+}
+
 template <typename T, int DP>
 hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
+  const int nt = (p.sv ? 1 : 0) + (p.dkk ? 1 : 0) + (p.dkv ? 1 : 0);
+  if (nt > 0 && tables_fit(nt, p.M, DP)) {
+    using S = TokShape<DP>;
+    const int BH = p.B * p.H;
+    const int nchunk = tok_chunks(BH, p.N, S::TPP);
+    const int passes = (p.N + S::TPP - 1) / S::TPP;
+    const int chunk_tokens = ((passes + nchunk - 1) / nchunk) * S::TPP;
+    const size_t lds = (size_t)nt * p.M * S::RSD * 4 + (size_t)p.M * 4;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&tok_bwd_lds_kernel<T, DP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
+    hipLaunchKernelGGL((tok_bwd_lds_kernel<T, DP>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk, chunk_tokens);
+    return hipGetLastError();
+  }
   constexpr int TPB = 256 / (DP / 8);
   dim3 grid((p.N + TPB - 1) / TPB, p.B * p.H);
   hipLaunchKernelGGL((tok_bwd_kernel<T, DP>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
+template <typename T, int DP, int PASSES, bool KV>
+hipError_t launch_tok_grad_lds(const TokGradParams& p, int nt, hipStream_t st) {
+  using S = TokShape<DP>;
+  const int BH = p.B * p.H;
+  const int nchunk = (p.N + PASSES * S::TPP - 1) / (PASSES * S::TPP);
+  const size_t lds = (size_t)nt * p.M * S::RSD * 4;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&tok_grad_lds_kernel<T, DP, PASSES, KV>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
+  hipLaunchKernelGGL((tok_grad_lds_kernel<T, DP, PASSES, KV>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
+  return hipGetLastError();
+}
+
 template <typename T, int DP>
 hipError_t launch_tok_grad_t(const TokGradParams& p, hipStream_t st) {
+  int nt = 0;  // most tables any round stages
+  for (int r = 0; r < p.R; ++r) {
+    const int k = ((p.ds[r] && p.dq.p) ? 1 : 0) + (p.dkk[r] ? 1 : 0) + (p.dkv[r] ? 1 : 0);
+    nt = k > nt ? k : nt;
+  }
+  if (nt > 0 && tables_fit(nt, p.M, DP)) {
+    // registers: dq only (the slot-key gradient terms go to dq) keeps 8 passes
+    // of tokens, with separate token-key / token-value gradients 4
+    if (p.shared_kv) return launch_tok_grad_lds<T, DP, 8, false>(p, nt, st);
+    return launch_tok_grad_lds<T, DP, 4, true>(p, nt, st);
+  }
   constexpr int TPB = 256 / (DP / 8);
   dim3 grid((p.N + TPB - 1) / TPB, p.B * p.H);
   hipLaunchKernelGGL((tok_grad_kernel<T, DP>), grid, dim3(256), 0, st, p);
