@@ -232,6 +232,32 @@ __device__ __forceinline__ void stage_table(float* __restrict__ dst, const float
   }
 }
 
+// 8 raw token elements (one or two 16-byte units), so loads for many tokens
+// can be in flight before any is converted
+template <typename T>
+struct Raw8 {
+  uint4 u[sizeof(T) / 2];
+};
+template <typename T>
+__device__ __forceinline__ Raw8<T> raw8(const T* __restrict__ row, int d0, int D, bool vec) {
+  Raw8<T> r;
+  if (vec && d0 + 8 <= D) {
+#pragma unroll
+    for (int k = 0; k < (int)(sizeof(T) / 2); ++k) r.u[k] = *reinterpret_cast<const uint4*>(row + d0 + k * (16 / sizeof(T)));
+  } else {
+    T* e = reinterpret_cast<T*>(&r);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = (d0 + i < D) ? row[d0 + i] : from_f<T>(0.f);
+  }
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ void unraw8(const Raw8<T>& r, float (&o)[8]) {
+  const T* e = reinterpret_cast<const T*>(&r);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = to_f(e[i]);
+}
+
 // 8 floats of a staged table row (16-byte aligned: d0 % 8 == 0)
 __device__ __forceinline__ void lds8(const float* __restrict__ row, int d0, float (&o)[8]) {
   const float4 a = *reinterpret_cast<const float4*>(row + d0);

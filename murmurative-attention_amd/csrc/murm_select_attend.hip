@@ -458,29 +458,24 @@ __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p,
     }
   }
   for (int r = 0; r < p.R; ++r) {
+    // the round's index rows and weights of every pass are requested before
+    // its table is staged
+    uint4 ix[GO_PASSES];
+    float wv[GO_PASSES][KN];
+#pragma unroll
+    for (int q = 0; q < GO_PASSES; ++q) {
+      const int n = min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1);
+      const int64_t row = (int64_t)bh * p.N + n;
+      ix[q] = *reinterpret_cast<const uint4*>(p.rp.idx[r] + row * IDX_ROW);
+#pragma unroll
+      for (int j = 0; j < KN; ++j) wv[q][j] = p.rp.w[r][row * KN + j];
+    }
     if (r > 0) __syncthreads();
     stage_table<DP>(tab, p.rp.a[r] + (int64_t)bh * p.M * p.D, p.M, p.D);
     __syncthreads();
-    // index rows and weights of pass q+1 are requested before pass q's gathers
-    uint4 irn;
-    float wn[KN];
-    auto fetch = [&](int q, uint4& ir, float (&w)[KN]) {
-      const int n = min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1);
-      const int64_t row = (int64_t)bh * p.N + n;
-      ir = *reinterpret_cast<const uint4*>(p.rp.idx[r] + row * IDX_ROW);
-#pragma unroll
-      for (int j = 0; j < KN; ++j) w[j] = p.rp.w[r][row * KN + j];
-    };
-    fetch(0, irn, wn);
 #pragma unroll
     for (int q = 0; q < GO_PASSES; ++q) {
-      const uint4 ir = irn;
-      float wc[KN];
-#pragma unroll
-      for (int j = 0; j < KN; ++j) wc[j] = wn[j];
-      if (q + 1 < GO_PASSES) fetch(q + 1, irn, wn);
-      const int n = c_beg + q * TPP + threadIdx.x / DCH;
-      if (n >= p.N) continue;
+      const uint4 ir = ix[q];
       const uint32_t sl[KN] = {ir.x & 0xFFFF, ir.x >> 16, ir.y & 0xFFFF, ir.y >> 16,
                                ir.z & 0xFFFF, ir.z >> 16, ir.w & 0xFFFF};
 #pragma unroll
@@ -488,7 +483,7 @@ __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p,
         float v[8];
         lds8(tab + sl[j] * RSD, d0, v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[q][i] += wc[j] * v[i];
+        for (int i = 0; i < 8; ++i) acc[q][i] += wv[q][j] * v[i];
       }
     }
   }

@@ -169,93 +169,106 @@ struct TokShape {
   static constexpr int RSD = DP + 4;                   // staged row stride
 };
 
-template <typename T, int DP>
-__global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams p, int nchunk, int chunk_tokens) {
+template <typename T, int DP, int NP, bool HV>
+__global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams p, int nchunk) {
   using S = TokShape<DP>;
   constexpr int DCH = S::DCH, TPP = S::TPP, RSD = S::RSD;
   extern __shared__ __align__(16) unsigned char smem[];
   int bh, chunk;
   if (!tok_block(p.B * p.H, nchunk, bh, chunk)) return;
   const int b = bh / p.H, h = bh % p.H;
-  const bool has_g = p.sv != nullptr, has_k = p.dkk != nullptr, has_v = p.dkv != nullptr;
-  float* t = reinterpret_cast<float*>(smem);
-  float* tsv = t;
+  const bool has_g = p.sv != nullptr, has_k = p.dkk != nullptr;
+  const int dc = threadIdx.x % DCH, d0 = dc * 8;
+  const int c_beg = chunk * NP * TPP;
+  // every global load of the block is issued first: index rows, token rows
+  // and (lane dc < 7) weight j = dc of each of the NP passes, then the tables
+  constexpr int JPL = (KN + DCH - 1) / DCH;  // weights finished per lane
+  uint4 ix[NP];
+  Raw8<T> rg[NP], rk[NP], rv[HV ? NP : 1];
+  float wq[NP][JPL], gq[NP][JPL];
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    const int n = min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1);
+    const int64_t row = (int64_t)bh * p.N + n;
+    ix[q] = *reinterpret_cast<const uint4*>(p.idx + row * IDX_ROW);
+    if (has_g) rg[q] = raw8<T>(tok_row<T>(p.g, b, h, n), d0, p.D, p.g.vec);
+    if (has_k) rk[q] = raw8<T>(tok_row<T>(p.tk, b, h, n), d0, p.D, p.tk.vec);
+    if constexpr (HV) rv[q] = raw8<T>(tok_row<T>(p.tv, b, h, n), d0, p.D, p.tv.vec);
+#pragma unroll
+    for (int u = 0; u < JPL; ++u) {
+      const int j = dc + u * DCH;
+      wq[q][u] = j < KN ? p.w[row * KN + j] : 0.f;
+      gq[q][u] = (p.gw && j < KN) ? p.gw[row * KN + j] : 0.f;
+    }
+  }
+  float* tsv = reinterpret_cast<float*>(smem);
   float* tdk = tsv + (has_g ? p.M * RSD : 0);
   float* tdv = tdk + (has_k ? p.M * RSD : 0);
-  float* tdw = tdv + (has_v ? p.M * RSD : 0);
+  float* tdw = tdv + (HV ? p.M * RSD : 0);
   const int64_t tb = (int64_t)bh * p.M * p.D;
   if (has_g) stage_table<DP>(tsv, p.sv + tb, p.M, p.D);
   if (has_k) stage_table<DP>(tdk, p.dkk + tb, p.M, p.D);
-  if (has_v) stage_table<DP>(tdv, p.dkv + tb, p.M, p.D);
+  if constexpr (HV) stage_table<DP>(tdv, p.dkv + tb, p.M, p.D);
   if (p.dW)
     for (int i = threadIdx.x; i < p.M; i += blockDim.x) tdw[i] = p.dW[(int64_t)bh * p.M + i];
   __syncthreads();
-  const int dc = threadIdx.x % DCH, d0 = dc * 8;
-  const int c_beg = chunk * chunk_tokens, c_end = min(p.N, c_beg + chunk_tokens);
-  // a pass's index row and token rows are requested during the previous pass
-  float gn[8], an[8], cn[8];
-  uint32_t sln[KN];
-  auto fetch = [&](int n0) {
-    const int n = min(n0 + (int)threadIdx.x / DCH, c_end - 1);
-    unpack_idx(p.idx + ((int64_t)bh * p.N + n) * IDX_ROW, sln);
-    if (has_g) load8<T>(tok_row<T>(p.g, b, h, n), d0, p.D, p.g.vec, gn);
-    if (has_k) load8<T>(tok_row<T>(p.tk, b, h, n), d0, p.D, p.tk.vec, an);
-    if (has_v) load8<T>(tok_row<T>(p.tv, b, h, n), d0, p.D, p.tv.vec, cn);
-  };
-  if (c_beg < c_end) fetch(c_beg);
-  for (int n0 = c_beg; n0 < c_end; n0 += TPP) {
-    const int n = n0 + threadIdx.x / DCH;
-    const bool live = n < c_end;
-    const int nn = live ? n : c_beg;
-    const int64_t row = (int64_t)bh * p.N + nn;
-    uint32_t sl[KN];
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    const int n = c_beg + q * TPP + threadIdx.x / DCH;
+    const uint4 ir = ix[q];
+    const uint32_t sl[KN] = {ir.x & 0xFFFF, ir.x >> 16, ir.y & 0xFFFF, ir.y >> 16,
+                             ir.z & 0xFFFF, ir.z >> 16, ir.w & 0xFFFF};
     float g[8], a[8], c[8];
-#pragma unroll
-    for (int j = 0; j < KN; ++j) sl[j] = sln[j];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) { g[i] = gn[i]; a[i] = an[i]; c[i] = cn[i]; }
-    if (n0 + TPP < c_end) fetch(n0 + TPP);
+    if (has_g) unraw8<T>(rg[q], g);
+    if (has_k) unraw8<T>(rk[q], a);
+    if constexpr (HV) unraw8<T>(rv[q], c);
     float dw[KN];
 #pragma unroll
     for (int j = 0; j < KN; ++j) {
-      float s = 0.f, v[8];
+      float sacc = 0.f, v[8];
       if (has_g) {
         lds8(tsv + sl[j] * RSD, d0, v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s += g[i] * v[i];
+        for (int i = 0; i < 8; ++i) sacc += g[i] * v[i];
       }
       if (has_k) {
         lds8(tdk + sl[j] * RSD, d0, v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s += a[i] * v[i];
+        for (int i = 0; i < 8; ++i) sacc += a[i] * v[i];
       }
-      if (has_v) {
+      if constexpr (HV) {
         lds8(tdv + sl[j] * RSD, d0, v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s += c[i] * v[i];
+        for (int i = 0; i < 8; ++i) sacc += c[i] * v[i];
       }
-      dw[j] = s;
+      dw[j] = group_sum<DCH>(sacc);
     }
+    // lane dc finishes weights j = dc, dc + DCH, ...
+    float mine[JPL];
+    float part = 0.f;
 #pragma unroll
-    for (int j = 0; j < KN; ++j) dw[j] = group_sum<DCH>(dw[j]);
-    if (live && dc == 0) {
+    for (int u = 0; u < JPL; ++u) {
+      const int jj = dc + u * DCH;
+      float m = dw[0];
+      uint32_t ms = sl[0];
 #pragma unroll
-      for (int j = 0; j < KN; ++j) {
-        if (p.dW) dw[j] += tdw[sl[j]];
-        if (p.gw) dw[j] += p.gw[row * KN + j];
+      for (int j = 1; j < KN; ++j) {
+        m = jj == j ? dw[j] : m;
+        ms = jj == j ? sl[j] : ms;
       }
-      if (p.dw_out) {
+      if (p.dW) m += tdw[ms];
+      m += gq[q][u];
+      mine[u] = m;
+      part += jj < KN ? wq[q][u] * m : 0.f;
+    }
+    const int64_t row = (int64_t)bh * p.N + n;
+    const float dot = p.ds_out ? group_sum<DCH>(part) : 0.f;
 #pragma unroll
-        for (int j = 0; j < KN; ++j) p.dw_out[row * KN + j] = dw[j];
-      }
-      if (p.ds_out) {
-        const float* w = p.w + row * KN;
-        float wj[KN], dot = 0.f;
-#pragma unroll
-        for (int j = 0; j < KN; ++j) { wj[j] = w[j]; dot += wj[j] * dw[j]; }
-#pragma unroll
-        for (int j = 0; j < KN; ++j) p.ds_out[row * KN + j] = wj[j] * (dw[j] - dot);
-      }
+    for (int u = 0; u < JPL; ++u) {
+      const int jj = dc + u * DCH;
+      if (jj >= KN || n >= p.N) continue;
+      if (p.dw_out) p.dw_out[row * KN + jj] = mine[u];
+      if (p.ds_out) p.ds_out[row * KN + jj] = wq[q][u] * (mine[u] - dot);
     }
   }
 }
@@ -421,29 +434,29 @@ inline bool tables_fit(int nt, int M, int DP) {
   return (size_t)nt * M * (DP + 4) * 4 + (size_t)M * 4 <= 150 * 1024;
 }
 
-// chunks per (b,h): about 256 blocks, whole passes per chunk
-inline int tok_chunks(int BH, int N, int tpp) {
-  const int passes = (N + tpp - 1) / tpp;
-  int c = (256 + BH - 1) / BH;
-  return c > passes ? passes : (c < 1 ? 1 : c);
+template <typename T, int DP, int NP, bool HV>
+hipError_t launch_tok_bwd_lds(const TokBwdParams& p, int nt, hipStream_t st) {
+  using S = TokShape<DP>;
+  const int BH = p.B * p.H;
+  const int nchunk = (p.N + NP * S::TPP - 1) / (NP * S::TPP);
+  const size_t lds = (size_t)nt * p.M * S::RSD * 4 + (size_t)p.M * 4;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&tok_bwd_lds_kernel<T, DP, NP, HV>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
+  hipLaunchKernelGGL((tok_bwd_lds_kernel<T, DP, NP, HV>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
+  return hipGetLastError();
 }
 
 template <typename T, int DP>
 hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
   const int nt = (p.sv ? 1 : 0) + (p.dkk ? 1 : 0) + (p.dkv ? 1 : 0);
   if (nt > 0 && tables_fit(nt, p.M, DP)) {
-    using S = TokShape<DP>;
-    const int BH = p.B * p.H;
-    const int nchunk = tok_chunks(BH, p.N, S::TPP);
-    const int passes = (p.N + S::TPP - 1) / S::TPP;
-    const int chunk_tokens = ((passes + nchunk - 1) / nchunk) * S::TPP;
-    const size_t lds = (size_t)nt * p.M * S::RSD * 4 + (size_t)p.M * 4;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&tok_bwd_lds_kernel<T, DP>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
-    hipLaunchKernelGGL((tok_bwd_lds_kernel<T, DP>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk, chunk_tokens);
-    return hipGetLastError();
+    // tokens per lane whose loads are all in flight at once: 8 (16-bit tokens,
+    // two token rows) or 4 (float32 tokens or three token rows)
+    if (p.dkv) return launch_tok_bwd_lds<T, DP, 4, true>(p, nt, st);
+    if (sizeof(T) == 2) return launch_tok_bwd_lds<T, DP, 8, false>(p, nt, st);
+    return launch_tok_bwd_lds<T, DP, 4, false>(p, nt, st);
   }
   constexpr int TPB = 256 / (DP / 8);
   dim3 grid((p.N + TPB - 1) / TPB, p.B * p.H);
