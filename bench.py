@@ -2,6 +2,9 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu]
 
+--config 2/3/4 run the op on BASELINE.json configs[1..3]; --config 5 runs the
+README MurmurativeAttention layer's training step.
+
 A step is one forward+backward of the README-form slot_murmurate over one
 synthetic batch (seeded N(0,1) draws), inputs resident
 in HBM.  `value` is tokens/s over exactly K timed steps (HIP-synchronised on
@@ -93,6 +96,97 @@ def measured_traffic(config):
     return out
 
 
+# config 5: the README's MurmurativeAttention layer (README.md:82-101) trained one step
+MODULE_CONFIGS = {
+    "5": {"dim": 1024, "heads": 16, "slots": 512, "B": 8, "N": 4096, "rounds": 3, "dtype": "bfloat16",
+          "lr": 5e-4, "eps": 1e-4},
+}
+
+
+def readme_module(torch, murmurate):
+    """The layer of README.md:82-101 over a given slot_murmurate implementation."""
+    nn = torch.nn
+
+    class MurmurativeAttention(nn.Module):
+        def __init__(self, dim, heads, slots, rounds=3):
+            super().__init__()
+            self.heads, self.slots, self.rounds = heads, slots, rounds
+            self.dim, self.head_dim = dim, dim // heads
+            self.q_proj = nn.Linear(dim, dim, bias=False)
+            self.o_proj = nn.Linear(dim, dim, bias=False)
+            self.slot_embeddings = nn.Parameter(torch.randn(heads, slots, self.head_dim))
+
+        def forward(self, x):
+            B, N, D = x.shape
+            q = self.q_proj(x).view(B, N, self.heads, self.head_dim).transpose(1, 2)
+            slots_k = self.slot_embeddings.unsqueeze(0).expand(B, -1, -1, -1)
+            slots_v = torch.zeros_like(slots_k)
+            attn_out = murmurate(q, slots_k, slots_v, self.rounds)[0]
+            return self.o_proj(attn_out.transpose(1, 2).contiguous().view(B, N, D))
+
+    return MurmurativeAttention
+
+
+def make_module(mc, device, batch=None, seed=42):
+    """Seeded layer + input + target: Linear weights ~ N(0, 0.02), slot embeddings
+    ~ N(0, 1), x and target ~ N(0, 1), drawn in fp32 on the CPU in that order."""
+    import torch
+    import murmurative
+    if device.type == "cuda":
+        fn = lambda q, k, v, r: murmurative.slot_murmurate(q, k, v, rounds=r)
+    else:
+        from oracle import murm_oracle as O
+        fn = lambda q, k, v, r: O.murmurate_readme(q, k, v, rounds=r)
+    dt = getattr(torch, mc["dtype"])
+    B = mc["B"] if batch is None else batch
+    g = torch.Generator().manual_seed(seed)
+    model = readme_module(torch, fn)(mc["dim"], mc["heads"], mc["slots"], mc["rounds"])
+    with torch.no_grad():
+        model.q_proj.weight.copy_(torch.randn(model.q_proj.weight.shape, generator=g) * 0.02)
+        model.o_proj.weight.copy_(torch.randn(model.o_proj.weight.shape, generator=g) * 0.02)
+        model.slot_embeddings.copy_(torch.randn(model.slot_embeddings.shape, generator=g))
+    x = torch.randn(B, mc["N"], mc["dim"], generator=g)
+    target = torch.randn(B, mc["N"], mc["dim"], generator=g)
+    model = model.to(device=device, dtype=dt)
+    opt = torch.optim.AdamW(model.parameters(), lr=mc["lr"], eps=mc["eps"])
+    return model, opt, x.to(device=device, dtype=dt), target.to(device=device, dtype=dt)
+
+
+def module_step(torch, model, opt, x, target):
+    opt.zero_grad(set_to_none=True)
+    loss = torch.nn.functional.mse_loss(model(x).float(), target.float())
+    loss.backward()
+    opt.step()
+    return loss
+
+
+def cpu_baseline_module(mc, budget_s=20.0):
+    """Time the same training step on the host with the CPU oracle in place of
+    the kernels: batch 1, the sequence length cut to fit the time budget."""
+    import torch
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    cpu = torch.device("cpu")
+
+    def run(n):
+        m = dict(mc, N=n)
+        model, opt, x, target = make_module(m, cpu, batch=1)
+        t0 = time.perf_counter()
+        module_step(torch, model, opt, x, target)
+        return time.perf_counter() - t0
+
+    run(256)  # warm-up
+    n = 256
+    while n < mc["N"] and run(n) * 2 * 3 < budget_s:
+        n *= 2
+    times = sorted(run(n) for _ in range(3))
+    med = times[1]
+    return {"value": round(n / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"README layer training step (MSE, AdamW) with oracle/murm_oracle.py murmurate_readme "
+                       f"in place of the kernels, {mc['dtype']}, B=1, N={n}, dim={mc['dim']}, heads={mc['heads']}, "
+                       f"slots={mc['slots']}, R={mc['rounds']}; median of 3, {med:.3f} s; tokens/s = N / time")}
+
+
 def make_inputs(cfg, device, seed=42):
     import torch
     B, H, N, D, M, R, causal, dt, sk_std, sv_std = cfg
@@ -139,7 +233,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="3", choices=sorted(list(CONFIGS) + list(MODULE_CONFIGS)))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -157,15 +251,25 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
-    cfg = CONFIGS[a.config]
-    B, H, N, D, M, R, causal, dt, _, _ = cfg
-    q, sk, sv, go = make_inputs(cfg, dev)
-    for t in (q, sk, sv):
-        t.requires_grad_(True)
+    module = a.config in MODULE_CONFIGS
+    if module:
+        mc = MODULE_CONFIGS[a.config]
+        B, N, M, R, dt = mc["B"], mc["N"], mc["slots"], mc["rounds"], mc["dtype"]
+        H, D, causal = mc["heads"], mc["dim"] // mc["heads"], False
+        model, opt, x, target = make_module(mc, dev)
 
-    def step():
-        out, idx, w = murmurative.slot_murmurate(q, sk, sv, rounds=R, causal=causal)
-        return torch.autograd.grad(out, (q, sk, sv), go)
+        def step():
+            return module_step(torch, model, opt, x, target)
+    else:
+        cfg = CONFIGS[a.config]
+        B, H, N, D, M, R, causal, dt, _, _ = cfg
+        q, sk, sv, go = make_inputs(cfg, dev)
+        for t in (q, sk, sv):
+            t.requires_grad_(True)
+
+        def step():
+            out, idx, w = murmurative.slot_murmurate(q, sk, sv, rounds=R, causal=causal)
+            return torch.autograd.grad(out, (q, sk, sv), go)
 
     for _ in range(a.warmup):
         step()
@@ -212,14 +316,24 @@ def main():
         kernels["select_attend"]["mfma_frac"] = round(tf / MFMA_BF16_PEAK_TFLOPS, 4)
     device_ms = sum(ms for ms, _ in kt.values()) / a.steps
 
+    dname = {"bfloat16": "bf16", "float16": "fp16", "float32": "fp32"}[dt]
+    if module:
+        metric = f"tokens/sec MurmurativeAttention layer training step dim={mc['dim']} heads={H} slots={M} {dname}"
+        data = "synthetic: seeded N(0,1) input and target, Linear weights ~ N(0,0.02), slot embeddings ~ N(0,1)"
+        config = {"workload": "README MurmurativeAttention layer: fwd + MSE + bwd + AdamW, BASELINE configs[4]",
+                  "B": B, "N": N, "dim": mc["dim"], "heads": H, "head_dim": D, "slots": M, "top_k": 7,
+                  "rounds": R, "lr": mc["lr"], "adam_eps": mc["eps"], "tokens_per_step": B * N}
+    else:
+        metric = METRIC if a.config == "3" else (
+            f"tokens/sec fwd+bwd slot_murmurate B={B} H={H} N={N} d={D} M={M}{' causal' if causal else ''} {dname}")
+        data = "synthetic: seeded N(0,1) draws shaped as BASELINE.json configs (slots_v ~ N(0,0.02))"
+        config = {"workload": f"slot_murmurate README form fwd+bwd, BASELINE configs[{int(a.config) - 1}]",
+                  "B": B, "H": H, "N": N, "head_dim": D, "M": M, "top_k": 7, "rounds": R, "causal": causal,
+                  "tokens_per_step": B * N}
     res = {
-        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
+        "metric": metric, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": {"bfloat16": "bf16", "float16": "fp16", "float32": "fp32"}[dt],
-        "data": "synthetic: seeded N(0,1) draws shaped as BASELINE.json configs (slots_v ~ N(0,0.02))",
-        "config": {"workload": f"slot_murmurate README form fwd+bwd, BASELINE configs[{int(a.config) - 1}]",
-                   "B": B, "H": H, "N": N, "head_dim": D, "M": M, "top_k": 7, "rounds": R, "causal": causal,
-                   "tokens_per_step": B * N},
+        "vs_baseline": None, "dtype": dname, "data": data, "config": config,
         "roofline": roofline,
         "kernels": kernels,
         "device_ms_per_step_in_kernels": round(device_ms, 4),
@@ -235,7 +349,7 @@ def main():
         res["copy_calibration_bytes_each_way"] = n * 4
         del src, dst
     if not a.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(cfg, a.cpu_budget)
+        res["cpu_baseline"] = cpu_baseline_module(mc, a.cpu_budget) if module else cpu_baseline(cfg, a.cpu_budget)
     print(json.dumps(res), flush=True)
     return 0
 
