@@ -61,7 +61,7 @@ struct SegParams {
 };
 
 struct PartParams {       // token-chunk partial sums (scratch)
-  int nchunk;             // chunks per (b,h); 0 = use the pull kernels
+  int nchunk;             // chunks per (b,h); 0 = none carved
   int chunk_tokens;       // tokens per chunk (multiple of the staging size)
   float* partA; float* partB; float* partW;  // [nchunk, BH, M, D] and [nchunk, BH, M]
 };
@@ -116,10 +116,10 @@ size_t sa_lds_bytes(int dtype, int DP, int M);
 hipError_t launch_attend_idx(int dtype, int DP, const AttendIdxParams& p, hipStream_t st);
 hipError_t launch_select_attend(int dtype, int DP, const SAParams& p, hipStream_t st);
 hipError_t launch_gather_out(int dtype, int DP, const OutParams& p, hipStream_t st);
-int seg_chunks(int B, int H, int N, int M, int D);   // 0: no token-chunk path for this shape
+int seg_chunks(int B, int H, int N, int M, int D);   // 0: shape not served (d > 128)
 int seg_chunk_tokens(int N, int nchunk);
-// stage 0: partial sums (token-chunk path) or the whole reduction (pull kernels);
-// stage 1: chunk reduction + epilogue, only when seg_two_stage() is true.
+// stage 0: token-chunk partial sums; stage 1: chunk reduction + epilogue.
+// seg_two_stage() is false when no chunk scratch was carved (launch_seg fails then).
 bool seg_two_stage(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp);
 hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp, int stage,
                       hipStream_t st);

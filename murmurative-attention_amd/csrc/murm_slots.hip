@@ -1,14 +1,10 @@
 // Slot-side kernels: deterministic per-slot reductions and the small
 // per-slot epilogues.
 //
-// seg kernels: one block (8 waves) owns a group of GS = 16 slots of one (b,h)
-// plus one halo slot on each side when a stencil follows.  It walks the
-// round's (token, j) -> slot entries in chunks of 2048 tokens: 64-bit LDS
-// bitmasks per 64-token group give every matching entry its rank (integer OR
-// is order-free), so each slot's entries land in an LDS list ordered by
-// token; the waves then gather the token rows of each list with four rows in
-// flight per lane and sum them in that order, finishing with a fixed
-// butterfly.  No float atomics: results are bitwise reproducible.
+// Slot reductions run in two launches per call: seg_partial sums the entries
+// of one token chunk per slot, seg_reduce adds the chunks in a fixed order and
+// runs the per-slot epilogue.  No float atomics: results are bitwise
+// reproducible.
 //   UPDATE   K_m = sum w*tk, V_m = sum w*tv, W_m = sum w, then the EMA
 //            (reference.py:86-115) and, with diffusion, the stencil over the
 //            post-update rows of the block (reference.py:118-135, 188-189).
@@ -31,23 +27,6 @@ namespace {
 
 constexpr int GS = 16;                 // owned slots per block
 constexpr int NSMAX = GS + 2;          // with halo
-constexpr int SEG_THREADS = 512;
-constexpr int SEG_WAVES = SEG_THREADS / 64;
-constexpr int CH = 4096;               // tokens per chunk (entry = token-local << 3 | j fits u16)
-constexpr int NGRP = CH / 64;          // 64-token groups per chunk (one per lane in the scans)
-static_assert(NGRP == 64, "the group prefix scan maps one group per lane");
-constexpr int TPT = CH / SEG_THREADS;  // tokens per thread in the scan
-constexpr int SPW = (NSMAX + SEG_WAVES - 1) / SEG_WAVES;  // slots per wave
-constexpr int UNR = 4;                 // rows in flight per lane
-
-struct SegShared {
-  unsigned long long masks[NGRP][NSMAX];
-  uint16_t goff[NGRP][NSMAX];
-  int cnt[NSMAX];
-  int loff[NSMAX];
-  uint16_t list[CH * KN];
-};
-
 __device__ __forceinline__ uint32_t idx_at(const uint4& r, int j) {
   const uint32_t w = j < 2 ? r.x : (j < 4 ? r.y : (j < 6 ? r.z : r.w));
   return (w >> (16 * (j & 1))) & 0xFFFF;
@@ -55,8 +34,8 @@ __device__ __forceinline__ uint32_t idx_at(const uint4& r, int j) {
 
 // 1-D grid, XCD-aware: workgroups are dispatched round-robin over the 8 XCDs
 // (linear id % 8), so every block of one (b,h) is placed on XCD bh % 8 and
-// the head's token rows, gathered about seven times over, stay in that
-// XCD's L2.  Blocks past the last head return before any barrier.
+// reads what the head's other blocks wrote or staged from that XCD's L2.
+// Blocks past the last head return before any barrier.
 constexpr int XCDS = 8;
 __device__ __forceinline__ bool seg_block(const SegParams& p, int& bh, int& g0) {
   const int G = (p.M + GS - 1) / GS;
@@ -66,160 +45,8 @@ __device__ __forceinline__ bool seg_block(const SegParams& p, int& bh, int& g0) 
   return bh < p.B * p.H;
 }
 
-template <typename T, int DP, int MODE>
-__device__ void seg_accumulate(const SegParams& p, int bh, int lo, int NS, SegShared& sh,
-                               float* accA, float* accB, float* accW) {
-  constexpr int DCH = DP / 8;        // 8-dim chunks per row
-  constexpr int ES = 64 / DCH;       // rows per wave step
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int es = lane / DCH, dc = lane % DCH;
-  const int d0 = dc * 8;
-  const int b = bh / p.H, h = bh % p.H;
-  const bool sameB = (MODE == SEG_UPDATE) && p.b_same_as_a;
-
-  float aA[SPW][8], aB[SPW][8], aW[SPW];
-#pragma unroll
-  for (int s = 0; s < SPW; ++s) {
-    aW[s] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) { aA[s][i] = 0.f; aB[s][i] = 0.f; }
-  }
-
-  const uint16_t* idxb = p.idx + (int64_t)bh * p.N * IDX_ROW;
-  const float* wb = p.wgt + (int64_t)bh * p.N * p.K;
-  const float* db = (MODE == SEG_ATTBWD) ? p.ds + (int64_t)bh * p.N * p.K : nullptr;
-  const unsigned long long below = (1ull << lane) - 1ull;
-
-  for (int c0 = 0; c0 < p.N; c0 += CH) {
-    for (int i = tid; i < NGRP * NSMAX; i += SEG_THREADS) (&sh.masks[0][0])[i] = 0ull;
-    __syncthreads();
-    uint4 rows[TPT];
-#pragma unroll
-    for (int i = 0; i < TPT; ++i) {
-      const int n = c0 + i * SEG_THREADS + tid;
-      rows[i] = (n < p.N) ? *reinterpret_cast<const uint4*>(idxb + (int64_t)n * IDX_ROW)
-                          : make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
-      const int grp = i * SEG_WAVES + wave;
-#pragma unroll
-      for (int j = 0; j < KN; ++j) {
-        const uint32_t s = idx_at(rows[i], j);
-        const uint32_t rel = s - (uint32_t)lo;
-        if (s != IDX_NONE && rel < (uint32_t)NS) atomicOr(&sh.masks[grp][rel], 1ull << lane);
-      }
-    }
-    __syncthreads();
-    // per slot: exclusive scan of the group popcounts (one group per lane)
-    for (int s = wave; s < NS; s += SEG_WAVES) {
-      const int c = __popcll(sh.masks[lane][s]);
-      int incl = c;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int t = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += t;
-      }
-      sh.goff[lane][s] = (uint16_t)(incl - c);
-      if (lane == 63) sh.cnt[s] = incl;
-    }
-    __syncthreads();
-    if (wave == 0) {  // slot offsets: exclusive scan over the NS counts
-      const int c = lane < NS ? sh.cnt[lane] : 0;
-      int incl = c;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int t = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += t;
-      }
-      if (lane < NS) sh.loff[lane] = incl - c;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < TPT; ++i) {
-      const int grp = i * SEG_WAVES + wave;
-#pragma unroll
-      for (int j = 0; j < KN; ++j) {
-        const uint32_t s = idx_at(rows[i], j);
-        const uint32_t rel = s - (uint32_t)lo;
-        if (s != IDX_NONE && rel < (uint32_t)NS) {
-          const int pos = sh.loff[rel] + sh.goff[grp][rel] + __popcll(sh.masks[grp][rel] & below);
-          sh.list[pos] = (uint16_t)(((i * SEG_THREADS + tid) << 3) | j);
-        }
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < SPW; ++s) {
-      const int rel = wave + SEG_WAVES * s;
-      if (rel >= NS) break;
-      const int beg = sh.loff[rel], end = beg + sh.cnt[rel];
-      for (int e0 = beg + es; e0 < end; e0 += ES * UNR) {
-        int nn[UNR], jj[UNR];
-        bool ok[UNR];
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-          const int e = e0 + u * ES;
-          ok[u] = e < end;
-          const uint32_t ent = ok[u] ? sh.list[e] : 0u;
-          nn[u] = c0 + (int)(ent >> 3);
-          jj[u] = (int)(ent & 7);
-        }
-        float ca[UNR], cb[UNR], va[UNR][8], vb[UNR][8];
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-          if (ok[u]) {
-            const int64_t o = (int64_t)nn[u] * p.K + jj[u];
-            cb[u] = wb[o];
-            ca[u] = (MODE == SEG_ATTBWD) ? p.ds_scale * db[o] : cb[u];
-            load8<T>(tok_row<T>(p.va, b, h, nn[u]), d0, p.D, p.va.vec, va[u]);
-            if (!sameB) load8<T>(tok_row<T>(p.vb, b, h, nn[u]), d0, p.D, p.vb.vec, vb[u]);
-          } else {
-            ca[u] = 0.f;
-            cb[u] = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) { va[u][i] = 0.f; vb[u][i] = 0.f; }
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) aA[s][i] += ca[u] * va[u][i];
-          if (!sameB) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) aB[s][i] += cb[u] * vb[u][i];
-          }
-          if (MODE == SEG_UPDATE) aW[s] += cb[u];
-        }
-      }
-    }
-    __syncthreads();
-  }
-
-  // fixed butterfly over the entry lanes, then lanes with es == 0 publish
-#pragma unroll
-  for (int s = 0; s < SPW; ++s) {
-    const int rel = wave + SEG_WAVES * s;
-#pragma unroll
-    for (int x = DCH; x < 64; x <<= 1) {
-      aW[s] += shfl_xor_f(aW[s], x);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        aA[s][i] += shfl_xor_f(aA[s][i], x);
-        aB[s][i] += shfl_xor_f(aB[s][i], x);
-      }
-    }
-    if (rel < NS && es == 0) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        accA[rel * DP + d0 + i] = aA[s][i];
-        accB[rel * DP + d0 + i] = sameB ? aA[s][i] : aB[s][i];
-      }
-      if (dc == 0) accW[rel] = aW[s];
-    }
-  }
-  __syncthreads();
-}
-
 // ---------------------------------------------------------------------------
-// Epilogues (shared by the pull kernels and the partial-sum reduction).  The
+// Epilogues of the chunk reduction.  The
 // block holds, in LDS, the sums of rows lo .. lo+NS-1 (lo = g0 - halo).
 // ---------------------------------------------------------------------------
 template <int DP>
@@ -341,34 +168,13 @@ __device__ void attbwd_epilogue(const SegParams& p, int bh, int g0, int halo, in
   }
 }
 
-// pull kernels: one block owns GS slots (+halo) and gathers their entries
-template <typename T, int DP>
-__global__ __launch_bounds__(SEG_THREADS) void seg_update_kernel(SegParams p) {
-  __shared__ SegShared sh;
-  __shared__ float accA[NSMAX * DP], accB[NSMAX * DP], accW[NSMAX];
-  int bh, g0;
-  if (!seg_block(p, bh, g0)) return;
-  const int halo = p.diffuse ? 1 : 0;
-  seg_accumulate<T, DP, SEG_UPDATE>(p, bh, g0 - halo, GS + 2 * halo, sh, accA, accB, accW);
-  update_epilogue<DP>(p, bh, g0, halo, GS + 2 * halo, accA, accB, accW);
-}
-
-template <typename T, int DP>
-__global__ __launch_bounds__(SEG_THREADS) void seg_attbwd_kernel(SegParams p) {
-  __shared__ SegShared sh;
-  __shared__ float accA[NSMAX * DP], accB[NSMAX * DP], accW[NSMAX];
-  int bh, g0;
-  if (!seg_block(p, bh, g0)) return;
-  const int halo = p.final_out ? 0 : 1;
-  seg_accumulate<T, DP, SEG_ATTBWD>(p, bh, g0 - halo, GS + 2 * halo, sh, accA, accB, accW);
-  attbwd_epilogue<DP>(p, bh, g0, halo, GS + 2 * halo, accA, accB);
-}
-
 // ---------------------------------------------------------------------------
 // Token-chunk path.
-// seg_partial: one block owns a token range of one (b,h) and every slot of
-// that head; thread (slot, vector, part) accumulates DP/TPS dims of one slot
-// sum in registers.  The range is walked in sub-chunks of SUB tokens: the
+// seg_partial: one block owns a token range of one (b,h) and one group of
+// that head's slots; thread (slot, vector, part) accumulates 32 dims of one
+// slot sum in registers.  Slot groups (at most 1024 threads a block) are
+// adjacent in launch order, so the blocks that stage the same token rows run
+// together and share them through L2.  The range is walked in sub-chunks of SUB tokens: the
 // token rows (16-byte units, coalesced), index rows and coefficient rows are
 // staged in LDS while the next sub-chunk's loads are already in flight in
 // registers; each token sets its slots' bits in 64-bit LDS masks (integer OR:
@@ -381,7 +187,6 @@ __global__ __launch_bounds__(SEG_THREADS) void seg_attbwd_kernel(SegParams p) {
 // partials are re-read from that XCD's L2.
 // ---------------------------------------------------------------------------
 constexpr int SUB = 128;    // tokens per staged sub-chunk
-constexpr int PF = 2;       // 16-byte row units prefetched per thread
 constexpr int CW = 8;       // coefficient row (7 used)
 constexpr int NCMAX = 16;   // chunks per (b,h)
 
@@ -397,10 +202,13 @@ __device__ __forceinline__ uint4 load_unit(const TokView& v, int b, int h, int n
   return r;
 }
 
-__device__ __forceinline__ void part_block(int nchunk, int BH, int& bh, int& chunk) {
+// 1-D grid: linear id % 8 = XCD = (b,h) % 8; then slot group, then chunk
+__device__ __forceinline__ void part_block(int nchunk, int nsg, int BH, int& bh, int& chunk, int& sg) {
   const int L = blockIdx.x, x = L % XCDS, k = L / XCDS;
-  bh = x + XCDS * (k / nchunk);
-  chunk = k % nchunk;
+  sg = k % nsg;
+  const int k2 = k / nsg;
+  bh = x + XCDS * (k2 / nchunk);
+  chunk = k2 % nchunk;
   if (bh >= BH) bh = -1;
 }
 
@@ -415,26 +223,31 @@ __device__ __forceinline__ void fma_row(float (&acc)[DP / TPS], float c, const u
   }
 }
 
-template <typename T, int DP, int TPS, int MODE>
-__global__ __launch_bounds__(DP / TPS <= 32 ? 1024 : 512) void seg_partial_kernel(SegParams p, PartParams pp) {
+template <typename T, int DP, int MODE>
+__global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartParams pp) {
   constexpr int ROW = DP + 8;                 // staged row stride (elements; bytes % 16 == 0)
+  constexpr int TPS = DP / 32;                // threads per (slot, vector)
   constexpr int DPT = DP / TPS;               // dims per thread
   constexpr int E = 16 / sizeof(T);           // elements per 16-byte unit
+  // 16-byte row units prefetched per thread (more spill at DP = 128 / fp32;
+  // stash() loads the remainder directly)
+  constexpr int PF = 2;
   constexpr int UPR = DP / E;                 // units per staged row
   constexpr int UPT = DPT / E;                // units per thread and token
   extern __shared__ __align__(16) unsigned char smem[];
   const bool sameB = (MODE == SEG_UPDATE) && p.b_same_as_a;
   const int nvec = sameB ? 1 : 2;
-  const int Mp = (p.M + 63) & ~63;
+  const int MS = blockDim.x / (TPS * nvec);                               // slots per block (multiple of 64)
+  const int nsg = (p.M + MS - 1) / MS;
   T* rows = reinterpret_cast<T*>(smem);                                   // [nvec][SUB][ROW]
   uint4* idxs = reinterpret_cast<uint4*>(rows + nvec * SUB * ROW);        // [SUB]
   float* cw = reinterpret_cast<float*>(idxs + SUB);                       // [SUB][CW] weights
   float* cd = cw + SUB * CW;                                              // [SUB][CW] c * ds
   unsigned long long* masks =
-      reinterpret_cast<unsigned long long*>(cd + (MODE == SEG_ATTBWD ? SUB * CW : 0));  // [SUB/64][Mp]
+      reinterpret_cast<unsigned long long*>(cd + (MODE == SEG_ATTBWD ? SUB * CW : 0));  // [SUB/64][MS]
 
-  int bh, chunk;
-  part_block(pp.nchunk, p.B * p.H, bh, chunk);
+  int bh, chunk, sg;
+  part_block(pp.nchunk, nsg, p.B * p.H, bh, chunk, sg);
   if (bh < 0) return;  // whole block, before any barrier
   const int b = bh / p.H, h = bh % p.H;
   const int c_beg = chunk * pp.chunk_tokens;
@@ -442,7 +255,8 @@ __global__ __launch_bounds__(DP / TPS <= 32 ? 1024 : 512) void seg_partial_kerne
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int part = tid % TPS;
   const int vec = (tid / TPS) % nvec;
-  const int slot = tid / (TPS * nvec);
+  const int s0 = sg * MS;
+  const int slot = s0 + tid / (TPS * nvec);
   const bool own = slot < p.M;
   const int nunits = nvec * SUB * UPR;
 
@@ -503,7 +317,7 @@ __global__ __launch_bounds__(DP / TPS <= 32 ? 1024 : 512) void seg_partial_kerne
       cw[i] = in ? p.wgt[(row0 + t) * KN + j] : 0.f;
       if (MODE == SEG_ATTBWD) cd[i] = in ? p.ds_scale * p.ds[(row0 + t) * KN + j] : 0.f;
     }
-    for (int i = tid; i < (SUB / 64) * Mp; i += nthr) masks[i] = 0ull;
+    for (int i = tid; i < (SUB / 64) * MS; i += nthr) masks[i] = 0ull;
   };
 
   float acc[DPT];
@@ -539,15 +353,15 @@ __global__ __launch_bounds__(DP / TPS <= 32 ? 1024 : 512) void seg_partial_kerne
       const uint4 ir = idxs[t];
 #pragma unroll
       for (int j = 0; j < KN; ++j) {
-        const uint32_t s = idx_at(ir, j);
-        if (s < (uint32_t)p.M) atomicOr(&masks[(t >> 6) * Mp + s], 1ull << (t & 63));
+        const uint32_t s = idx_at(ir, j) - (uint32_t)s0;  // slots of this group; others wrap past MS
+        if (s < (uint32_t)MS && s + s0 < (uint32_t)p.M) atomicOr(&masks[(t >> 6) * MS + s], 1ull << (t & 63));
       }
     }
     __syncthreads();
     if (own) {
 #pragma unroll
       for (int g = 0; g < SUB / 64; ++g) {
-        unsigned long long mk = masks[g * Mp + slot];
+        unsigned long long mk = masks[g * MS + (slot - s0)];
         while (mk) {
           const int t = g * 64 + (int)__builtin_ctzll(mk);
           mk &= mk - 1ull;
@@ -782,33 +596,33 @@ __global__ void stencil_kernel(T* __restrict__ x, int64_t sb, int64_t sh, int64_
   }
 }
 
-// Threads per (slot, vector) of the token-chunk path: 32 dims each when the
-// block fits 1024 threads, else 64 dims each in at most 512 threads (register
-// budget); 0 = use the pull kernels.
-int part_tps(int DP, int M, int nvec) {
+// Slots per block of the token-chunk path: 32 dims per thread, at most 1024
+// threads, slot groups of equal size (multiples of 64).
+int part_slots(int DP, int M, int nvec) {
+  const int maxs = 1024 / (nvec * (DP / 32));
   const int Mp = (M + 63) & ~63;
-  if (Mp * nvec * (DP / 32) <= 1024) return DP / 32;              // 32 dims per thread
-  if (DP >= 64 && Mp * nvec * (DP / 64) <= 512) return DP / 64;   // 64 dims, 512 threads at most
-  return 0;
+  const int nsg = (Mp + maxs - 1) / maxs;
+  return (((Mp + nsg - 1) / nsg) + 63) & ~63;
 }
 
 template <typename T, int DP>
-size_t part_lds_bytes(int M, int mode, int nvec) {
-  const size_t Mp = (size_t)((M + 63) & ~63);
+size_t part_lds_bytes(int MS, int mode, int nvec) {
   return (size_t)nvec * SUB * (DP + 8) * sizeof(T) + SUB * 16 + (size_t)SUB * CW * 4 * (mode == SEG_ATTBWD ? 2 : 1) +
-         (SUB / 64) * Mp * 8;
+         (SUB / 64) * (size_t)MS * 8;
 }
 
-template <typename T, int DP, int TPS, int MODE>
-hipError_t launch_part(const SegParams& p, const PartParams& pp, int nvec, size_t lds, int stage, hipStream_t st) {
+template <typename T, int DP, int MODE>
+hipError_t launch_part(const SegParams& p, const PartParams& pp, int nvec, int MS, size_t lds, int stage,
+                       hipStream_t st) {
   const int BH = p.B * p.H;
   if (stage == 0) {
-    const void* fn = reinterpret_cast<const void*>(&seg_partial_kernel<T, DP, TPS, MODE>);
+    const void* fn = reinterpret_cast<const void*>(&seg_partial_kernel<T, DP, MODE>);
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk);
-    const int threads = ((p.M + 63) & ~63) * nvec * TPS;
-    hipLaunchKernelGGL((seg_partial_kernel<T, DP, TPS, MODE>), grid, dim3(threads), lds, st, p, pp);
+    const int nsg = (p.M + MS - 1) / MS;
+    dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk * nsg);
+    const int threads = MS * nvec * (DP / 32);
+    hipLaunchKernelGGL((seg_partial_kernel<T, DP, MODE>), grid, dim3(threads), lds, st, p, pp);
   } else {
     const int G = (p.M + GS - 1) / GS;
     hipLaunchKernelGGL((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G), dim3(256), 0,
@@ -817,43 +631,24 @@ hipError_t launch_part(const SegParams& p, const PartParams& pp, int nvec, size_
   return hipGetLastError();
 }
 
-template <typename T, int DP, int MODE>
-hipError_t launch_part_tps(const SegParams& p, const PartParams& pp, int nvec, int tps, size_t lds, int stage,
-                           hipStream_t st) {
-  if constexpr (DP == 32) {
-    return launch_part<T, 32, 1, MODE>(p, pp, nvec, lds, stage, st);
-  } else {
-    if (tps == DP / 32) return launch_part<T, DP, DP / 32, MODE>(p, pp, nvec, lds, stage, st);
-    return launch_part<T, DP, DP / 64, MODE>(p, pp, nvec, lds, stage, st);
-  }
-}
-
 template <typename T, int DP>
-bool part_ok(const SegParams& p, int mode, const PartParams* pp, int& nvec, int& tps, size_t& lds) {
+bool part_ok(const SegParams& p, int mode, const PartParams* pp, int& nvec, int& MS, size_t& lds) {
   nvec = (mode == SEG_UPDATE && p.b_same_as_a) ? 1 : 2;
-  tps = part_tps(DP, p.M, nvec);
-  lds = part_lds_bytes<T, DP>(p.M, mode, nvec);
-  return pp && pp->nchunk > 0 && tps > 0 && lds <= 160 * 1024;
+  MS = part_slots(DP, p.M, nvec);
+  lds = part_lds_bytes<T, DP>(MS, mode, nvec);
+  return pp && pp->nchunk > 0 && lds <= 160 * 1024;
 }
 
-// stage 0: the partial-sum kernel (token-chunk path) or the whole pull kernel;
-// stage 1: the chunk reduction with the epilogue (token-chunk path only).
+// stage 0: the partial-sum kernel; stage 1: the chunk reduction with the epilogue.
 template <typename T, int DP>
 hipError_t launch_seg_t(const SegParams& p, int mode, const PartParams* pp, int stage, hipStream_t st) {
-  int nvec, tps;
+  int nvec, MS;
   size_t lds;
-  if (part_ok<T, DP>(p, mode, pp, nvec, tps, lds)) {
-    if (mode == SEG_UPDATE) return launch_part_tps<T, DP, SEG_UPDATE>(p, *pp, nvec, tps, lds, stage, st);
-    return launch_part_tps<T, DP, SEG_ATTBWD>(p, *pp, nvec, tps, lds, stage, st);
+  if (part_ok<T, DP>(p, mode, pp, nvec, MS, lds)) {
+    if (mode == SEG_UPDATE) return launch_part<T, DP, SEG_UPDATE>(p, *pp, nvec, MS, lds, stage, st);
+    return launch_part<T, DP, SEG_ATTBWD>(p, *pp, nvec, MS, lds, stage, st);
   }
-  if (stage != 0) return hipSuccess;
-  const int G = (p.M + GS - 1) / GS;
-  dim3 grid(XCDS * ((p.B * p.H + XCDS - 1) / XCDS) * G);
-  if (mode == SEG_UPDATE)
-    hipLaunchKernelGGL((seg_update_kernel<T, DP>), grid, dim3(SEG_THREADS), 0, st, p);
-  else
-    hipLaunchKernelGGL((seg_attbwd_kernel<T, DP>), grid, dim3(SEG_THREADS), 0, st, p);
-  return hipGetLastError();
+  return hipErrorInvalidValue;  // no chunk scratch carved, or d > 128
 }
 
 inline int grid1d(int64_t n, int tpb = 256) {
@@ -864,13 +659,13 @@ inline int grid1d(int64_t n, int tpb = 256) {
 }  // namespace
 
 bool seg_two_stage(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp) {
-  int nvec, tps;
+  int nvec, MS;
   size_t lds;
 #define MURM_SEGQ(T)                                                   \
   switch (DP) {                                                        \
-    case 32: return part_ok<T, 32>(p, mode, pp, nvec, tps, lds);       \
-    case 64: return part_ok<T, 64>(p, mode, pp, nvec, tps, lds);       \
-    case 128: return part_ok<T, 128>(p, mode, pp, nvec, tps, lds);     \
+    case 32: return part_ok<T, 32>(p, mode, pp, nvec, MS, lds);        \
+    case 64: return part_ok<T, 64>(p, mode, pp, nvec, MS, lds);        \
+    case 128: return part_ok<T, 128>(p, mode, pp, nvec, MS, lds);      \
     default: return false;                                             \
   }
   switch (dtype) {
@@ -883,9 +678,8 @@ bool seg_two_stage(int dtype, int DP, int mode, const SegParams& p, const PartPa
 }
 
 int seg_chunks(int B, int H, int N, int M, int D) {
-  // token-chunk path: about 256 blocks of whole sub-chunks, at most NCMAX per (b,h)
-  const int DP = D <= 32 ? 32 : (D <= 64 ? 64 : 128);
-  if (part_tps(DP, M, 1) == 0) return 0;
+  // token-chunk path: about 256 (b,h,chunk) blocks of whole sub-chunks, at most NCMAX per (b,h)
+  if (D > 128 || M < 1) return 0;
   const int BH = B * H;
   const int per = (N + SUB - 1) / SUB;
   int c = (256 + BH - 1) / BH;

@@ -84,8 +84,9 @@ SMALL = [
     (torch.bfloat16, 1, 2, 128, 128, 256, 3, True),
     (torch.float16, 1, 1, 64, 64, 512, 4, False),
     (torch.bfloat16, 2, 1, 1100, 64, 256, 1, False),
-    # M = 520: the backward's slot reduction takes the per-slot-group kernels
+    # M = 520 and d = 128: the slot reductions split the slots over several blocks per token chunk
     (torch.bfloat16, 1, 2, 160, 64, 520, 3, False),
+    (torch.bfloat16, 1, 2, 2048, 128, 256, 3, True),
 ]
 
 
