@@ -245,6 +245,7 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
   float* cd = cw + SUB * CW;                                              // [SUB][CW] c * ds
   unsigned long long* masks =
       reinterpret_cast<unsigned long long*>(cd + (MODE == SEG_ATTBWD ? SUB * CW : 0));  // [SUB/64][MS]
+  uint8_t* jt = reinterpret_cast<uint8_t*>(masks + (SUB / 64) * MS);  // [SUB][MS]: j naming the slot
 
   int bh, chunk, sg;
   part_block(pp.nchunk, nsg, p.B * p.H, bh, chunk, sg);
@@ -327,17 +328,6 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
   const T* vrows = rows + vec * SUB * ROW + part * DPT;
   const float* coef = (MODE == SEG_ATTBWD && vec == 0) ? cd : cw;
   const bool wacc = (MODE == SEG_UPDATE) && vec == 0 && part == 0;
-  const uint32_t me = (uint32_t)slot;
-  // coefficient of this slot in token t: the sum over every j that names it
-  // (more than one j only with caller-given indices), in j order
-  auto coef_of = [&](int t, const uint4& ir) {
-    uint32_t mb = 0;
-#pragma unroll
-    for (int j = 0; j < KN; ++j) mb |= (idx_at(ir, j) == me ? 1u : 0u) << j;
-    float c = coef[t * CW + __builtin_ctz(mb | 0x80u)];
-    for (uint32_t r = mb & (mb - 1u); r; r &= r - 1u) c += coef[t * CW + __builtin_ctz(r)];
-    return c;
-  };
   auto row_of = [&](int t, uint4 (&x)[UPT]) {
 #pragma unroll
     for (int u = 0; u < UPT; ++u) x[u] = *reinterpret_cast<const uint4*>(vrows + t * ROW + u * E);
@@ -349,13 +339,34 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
     stash(n0);
     __syncthreads();
     if (n0 + SUB < c_end) fetch(n0 + SUB);  // in flight during marking and the walk
-    for (int t = tid; t < cnt; t += nthr) {
+    // one thread per (token, j): the first j naming a slot of this group sets
+    // the token's bit and records j; later js naming the same slot (caller-
+    // given indices only) add their coefficients to the first one's, in j order
+    for (int i = tid; i < cnt * CW; i += nthr) {
+      const int t = i / CW, j = i % CW;
       const uint4 ir = idxs[t];
+      const uint32_t sj = idx_at(ir, j);
+      const uint32_t s = sj - (uint32_t)s0;  // slots of this group; others wrap past MS
+      if (j >= KN || s >= (uint32_t)MS || sj >= (uint32_t)p.M) continue;
+      uint32_t before = 0, after = 0;
 #pragma unroll
-      for (int j = 0; j < KN; ++j) {
-        const uint32_t s = idx_at(ir, j) - (uint32_t)s0;  // slots of this group; others wrap past MS
-        if (s < (uint32_t)MS && s + s0 < (uint32_t)p.M) atomicOr(&masks[(t >> 6) * MS + s], 1ull << (t & 63));
+      for (int q = 0; q < KN; ++q) {
+        const uint32_t hit = idx_at(ir, q) == sj ? 1u : 0u;
+        before |= (q < j ? hit : 0u) << q;
+        after |= (q > j ? hit : 0u) << q;
       }
+      if (before) continue;
+      if (after) {
+        float a = cw[t * CW + j], c = MODE == SEG_ATTBWD ? cd[t * CW + j] : 0.f;
+        for (uint32_t r = after; r; r &= r - 1u) {
+          a += cw[t * CW + __builtin_ctz(r)];
+          if (MODE == SEG_ATTBWD) c += cd[t * CW + __builtin_ctz(r)];
+        }
+        cw[t * CW + j] = a;
+        if (MODE == SEG_ATTBWD) cd[t * CW + j] = c;
+      }
+      atomicOr(&masks[(t >> 6) * MS + s], 1ull << (t & 63));
+      jt[t * MS + s] = (uint8_t)j;
     }
     __syncthreads();
     if (own) {
@@ -366,9 +377,8 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
           const int t = g * 64 + (int)__builtin_ctzll(mk);
           mk &= mk - 1ull;
           uint4 x[UPT];
-          const uint4 ir = idxs[t];
           row_of(t, x);
-          const float a = coef_of(t, ir);
+          const float a = coef[t * CW + jt[t * MS + (slot - s0)]];
           fma_row<T, DP, TPS>(acc, a, x);
           if (wacc) accw += a;
         }
@@ -608,7 +618,7 @@ int part_slots(int DP, int M, int nvec) {
 template <typename T, int DP>
 size_t part_lds_bytes(int MS, int mode, int nvec) {
   return (size_t)nvec * SUB * (DP + 8) * sizeof(T) + SUB * 16 + (size_t)SUB * CW * 4 * (mode == SEG_ATTBWD ? 2 : 1) +
-         (SUB / 64) * (size_t)MS * 8;
+         (SUB / 64) * (size_t)MS * 8 + (size_t)SUB * MS;
 }
 
 template <typename T, int DP, int MODE>
@@ -636,6 +646,10 @@ bool part_ok(const SegParams& p, int mode, const PartParams* pp, int& nvec, int&
   nvec = (mode == SEG_UPDATE && p.b_same_as_a) ? 1 : 2;
   MS = part_slots(DP, p.M, nvec);
   lds = part_lds_bytes<T, DP>(MS, mode, nvec);
+  while (lds > 160 * 1024 && MS > 64) {  // fp32 rows at d = 128: smaller slot groups
+    MS -= 64;
+    lds = part_lds_bytes<T, DP>(MS, mode, nvec);
+  }
   return pp && pp->nchunk > 0 && lds <= 160 * 1024;
 }
 
