@@ -189,6 +189,16 @@ __device__ void attbwd_epilogue(const SegParams& p, int bh, int g0, int halo, in
 constexpr int SUB = 128;    // tokens per staged sub-chunk
 constexpr int CW = 8;       // coefficient row (7 used)
 constexpr int NCMAX = 16;   // chunks per (b,h)
+// reduction threads: with many chunks every (vector, row, 4 dims) item of a
+// group gets its own thread (up to 1024), so all chunk loads are in flight at
+// once; with few chunks (many heads) 256-thread blocks keep more groups resident
+constexpr int RED_THREADS = 1024;
+inline int red_threads(int nchunk, int DP) {
+  if (nchunk < 8) return 256;
+  const int items = 2 * NSMAX * (DP / 4);
+  const int t = (items + 63) & ~63;
+  return t > RED_THREADS ? RED_THREADS : t;
+}
 
 template <typename T>
 __device__ __forceinline__ uint4 load_unit(const TokView& v, int b, int h, int n, int e0, int D) {
@@ -212,17 +222,6 @@ __device__ __forceinline__ void part_block(int nchunk, int nsg, int BH, int& bh,
   if (bh >= BH) bh = -1;
 }
 
-template <typename T, int DP, int TPS>
-__device__ __forceinline__ void fma_row(float (&acc)[DP / TPS], float c, const uint4 (&x)[DP / TPS * sizeof(T) / 16]) {
-  constexpr int DPT = DP / TPS, E = 16 / sizeof(T);
-#pragma unroll
-  for (int u = 0; u < DPT / E; ++u) {
-    const T* e = reinterpret_cast<const T*>(&x[u]);
-#pragma unroll
-    for (int i = 0; i < E; ++i) acc[u * E + i] += c * to_f(e[i]);
-  }
-}
-
 template <typename T, int DP, int MODE>
 __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartParams pp) {
   constexpr int ROW = DP + 8;                 // staged row stride (elements; bytes % 16 == 0)
@@ -233,7 +232,7 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
   // stash() loads the remainder directly)
   constexpr int PF = 2;
   constexpr int UPR = DP / E;                 // units per staged row
-  constexpr int UPT = DPT / E;                // units per thread and token
+  constexpr int UPT = DPT / E;                // 16-byte units per thread and token
   extern __shared__ __align__(16) unsigned char smem[];
   const bool sameB = (MODE == SEG_UPDATE) && p.b_same_as_a;
   const int nvec = sameB ? 1 : 2;
@@ -328,9 +327,15 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
   const T* vrows = rows + vec * SUB * ROW + part * DPT;
   const float* coef = (MODE == SEG_ATTBWD && vec == 0) ? cd : cw;
   const bool wacc = (MODE == SEG_UPDATE) && vec == 0 && part == 0;
-  auto row_of = [&](int t, uint4 (&x)[UPT]) {
+  // acc += a * (this thread's dims of staged row t), one 16-byte unit at a time
+  auto fma_staged = [&](int t, float a) {
 #pragma unroll
-    for (int u = 0; u < UPT; ++u) x[u] = *reinterpret_cast<const uint4*>(vrows + t * ROW + u * E);
+    for (int u = 0; u < UPT; ++u) {
+      const uint4 x = *reinterpret_cast<const uint4*>(vrows + t * ROW + u * E);
+      const T* e = reinterpret_cast<const T*>(&x);
+#pragma unroll
+      for (int i = 0; i < E; ++i) acc[u * E + i] += a * to_f(e[i]);
+    }
   };
 
   fetch(c_beg);
@@ -376,10 +381,8 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
         while (mk) {
           const int t = g * 64 + (int)__builtin_ctzll(mk);
           mk &= mk - 1ull;
-          uint4 x[UPT];
-          row_of(t, x);
           const float a = coef[t * CW + jt[t * MS + (slot - s0)]];
-          fma_row<T, DP, TPS>(acc, a, x);
+          fma_staged(t, a);
           if (wacc) accw += a;
         }
       }
@@ -402,7 +405,7 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
 }
 
 template <int DP, int MODE>
-__global__ __launch_bounds__(256) void seg_reduce_kernel(SegParams p, PartParams pp) {
+__global__ __launch_bounds__(RED_THREADS) void seg_reduce_kernel(SegParams p, PartParams pp) {
   __shared__ float accA[NSMAX * DP], accB[NSMAX * DP], accW[NSMAX];
   int bh, g0;
   if (!seg_block(p, bh, g0)) return;
@@ -635,7 +638,8 @@ hipError_t launch_part(const SegParams& p, const PartParams& pp, int nvec, int M
     hipLaunchKernelGGL((seg_partial_kernel<T, DP, MODE>), grid, dim3(threads), lds, st, p, pp);
   } else {
     const int G = (p.M + GS - 1) / GS;
-    hipLaunchKernelGGL((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G), dim3(256), 0,
+    hipLaunchKernelGGL((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G),
+                       dim3(red_threads(pp.nchunk, DP)), 0,
                        st, p, pp);
   }
   return hipGetLastError();
