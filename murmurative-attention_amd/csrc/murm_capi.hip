@@ -371,8 +371,11 @@ int murm_select_attend_fwd(int dtype, int slot_dtype, int B, int H, int N, int D
   if (sa_lds_bytes(dtype, DP, M) > 160 * 1024)
     return fail(MURM_ERR_UNSUPPORTED, "slot keys (M=%d, D=%d) exceed the 160 KiB LDS of one CU", M, D);
   hipStream_t st = (hipStream_t)stream;
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sk, sk_sb, sk_sh, sk_sm, L.sk, B, H, M, D, st));
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sv, sv_sb, sv_sh, sv_sm, L.sv, B, H, M, D, st));
+  {
+    const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk};
+    const SlotConv<const void*, float*> cb{sv, sv_sb, sv_sh, sv_sm, L.sv};
+    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+  }
   SAParams p = sa_params(B, H, N, D, M, tv_of(q, q_sb, q_sh, q_sn, dtype), L.sk, effective_M, causal, scale);
   p.mask = mask; p.mk_sb = mk_sb; p.mk_sh = mk_sh; p.mk_sn = mk_sn; p.mk_sm = mk_sm;
   p.bias = bias; p.bs_sb = bs_sb; p.bs_sh = bs_sh; p.bs_sn = bs_sn; p.bs_sm = bs_sm;
@@ -424,8 +427,11 @@ int murm_attend_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, int M
   const int DP = pick_dp(D);
   hipStream_t st = (hipStream_t)stream;
   RUN(C_CONV, "idx_pack", launch_idx_pack(indices, L.idx, (int64_t)B * H * N, KN, M, st));
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sk, sk_sb, sk_sh, sk_sm, L.sk, B, H, M, D, st));
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sv, sv_sb, sv_sh, sv_sm, L.sv, B, H, M, D, st));
+  {
+    const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk};
+    const SlotConv<const void*, float*> cb{sv, sv_sb, sv_sh, sv_sm, L.sv};
+    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+  }
   AttendIdxParams a{};
   a.B = B; a.H = H; a.N = N; a.D = D; a.M = M;
   a.q = tv_of(q, q_sb, q_sh, q_sn, dtype); a.sk = L.sk; a.idx = L.idx;
@@ -463,8 +469,11 @@ int murm_select_attend_bwd(int dtype, int slot_dtype, int B, int H, int N, int D
   const float c = scale > 0 ? (float)scale : (float)(1.0 / sqrt((double)D));
   const int64_t rows = (int64_t)B * H * N;
   RUN(C_CONV, "idx_pack", launch_idx_pack(indices, L.idx, rows, KN, M, st));
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sk, sk_sb, sk_sh, sk_sm, L.sk, B, H, M, D, st));
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sv, sv_sb, sv_sh, sv_sm, L.sv, B, H, M, D, st));
+  {
+    const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk};
+    const SlotConv<const void*, float*> cb{sv, sv_sb, sv_sh, sv_sm, L.sv};
+    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+  }
   const TokView g = tv_of(grad_out, g_sb, g_sh, g_sn, dtype);
   const TokView qv = tv_of(q, q_sb, q_sh, q_sn, dtype);
   TokBwdParams t{};
@@ -478,8 +487,11 @@ int murm_select_attend_bwd(int dtype, int slot_dtype, int B, int H, int N, int D
   if (seg_two_stage(dtype, DP, SEG_ATTBWD, s, &L.part))
     RUN(C_SEGBR, "seg_attbwd_reduce", launch_seg(dtype, DP, SEG_ATTBWD, s, &L.part, 1, st));
   const int64_t ssb = (int64_t)H * M * D, ssh = (int64_t)M * D, ssm = D;
-  RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.dk, grad_sk, ssb, ssh, ssm, B, H, M, D, st));
-  RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.dv, grad_sv, ssb, ssh, ssm, B, H, M, D, st));
+  {
+    const SlotConv<const float*, void*> ca{L.dk, ssb, ssh, ssm, grad_sk};
+    const SlotConv<const float*, void*> cb{L.dv, ssb, ssh, ssm, grad_sv};
+    RUN(C_CONV, "from_state", launch_from_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+  }
   TokGradParams tg{};
   tg.B = B; tg.H = H; tg.N = N; tg.D = D; tg.M = M; tg.R = 1; tg.c = c;
   tg.g = none_tv();
@@ -509,8 +521,11 @@ static int update_common(int dtype, int slot_dtype, int B, int H, int N, int D, 
   const int DP = pick_dp(D);
   hipStream_t st = (hipStream_t)stream;
   RUN(C_CONV, "idx_pack", launch_idx_pack(indices, L.idx, (int64_t)B * H * N, KN, M, st));
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sk, sk_sb, sk_sh, sk_sm, L.sk, B, H, M, D, st));
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sv, sv_sb, sv_sh, sv_sm, L.sv, B, H, M, D, st));
+  {
+    const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk};
+    const SlotConv<const void*, float*> cb{sv, sv_sb, sv_sh, sv_sm, L.sv};
+    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+  }
   SegParams s = seg_base(B, H, N, D, M);
   s.idx = L.idx; s.wgt = weights;
   s.va = tv_of(tk, tk_sb, tk_sh, tk_sn, dtype);
@@ -521,8 +536,11 @@ static int update_common(int dtype, int slot_dtype, int B, int H, int N, int D, 
   RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, 0, st));
   if (seg_two_stage(dtype, DP, SEG_UPDATE, s, &L.part))
     RUN(C_SEGUR, "seg_update_reduce", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, 1, st));
-  RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.nk, sk, sk_sb, sk_sh, sk_sm, B, H, M, D, st));
-  RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.nv, sv, sv_sb, sv_sh, sv_sm, B, H, M, D, st));
+  {
+    const SlotConv<const float*, void*> ca{L.nk, sk_sb, sk_sh, sk_sm, sk};
+    const SlotConv<const float*, void*> cb{L.nv, sv_sb, sv_sh, sv_sm, sv};
+    RUN(C_CONV, "from_state", launch_from_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+  }
   return MURM_OK;
 }
 
@@ -569,8 +587,11 @@ int murm_slot_update_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, 
   const int DP = pick_dp(D);
   hipStream_t st = (hipStream_t)stream;
   RUN(C_CONV, "idx_pack", launch_idx_pack(indices, L.idx, (int64_t)B * H * N, KN, M, st));
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, gk, gk_sb, gk_sh, gk_sm, L.sk, B, H, M, D, st));
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, gv, gv_sb, gv_sh, gv_sm, L.sv, B, H, M, D, st));
+  {
+    const SlotConv<const void*, float*> ca{gk, gk_sb, gk_sh, gk_sm, L.sk};
+    const SlotConv<const void*, float*> cb{gv, gv_sb, gv_sh, gv_sm, L.sv};
+    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+  }
   const TokView tkv = tv_of(tk, tk_sb, tk_sh, tk_sn, dtype);
   const TokView tvv = tv_of(tv, tv_sb, tv_sh, tv_sn, dtype);
   SegParams s = seg_base(B, H, N, D, M);
@@ -586,8 +607,11 @@ int murm_slot_update_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, 
   d.dk_out = L.dk; d.dv_out = L.dv; d.dW_out = L.dW; d.carry_k = L.ck; d.carry_v = L.cv;
   RUN(C_DU, "du", launch_du(d, st));
   const int64_t ssb = (int64_t)H * M * D, ssh = (int64_t)M * D, ssm = D;
-  RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.ck, grad_old_sk, ssb, ssh, ssm, B, H, M, D, st));
-  RUN(C_CONV, "from_state", launch_from_state(slot_dtype, L.cv, grad_old_sv, ssb, ssh, ssm, B, H, M, D, st));
+  {
+    const SlotConv<const float*, void*> ca{L.ck, ssb, ssh, ssm, grad_old_sk};
+    const SlotConv<const float*, void*> cb{L.cv, ssb, ssh, ssm, grad_old_sv};
+    RUN(C_CONV, "from_state", launch_from_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+  }
   TokBwdParams t{};
   t.B = B; t.H = H; t.N = N; t.D = D; t.M = M;
   t.tk = tkv; t.tv = tvv; t.idx = L.idx; t.w = weights;
@@ -663,8 +687,11 @@ int murm_murmurate_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
   const TokView qv = tv_of(q, q_sb, q_sh, q_sn, dtype);
   const TokView kv = shared ? qv : tv_of(tk, tk_sb, tk_sh, tk_sn, dtype);
   const TokView vv = shared ? qv : tv_of(tv, tv_sb, tv_sh, tv_sn, dtype);
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sk, sk_sb, sk_sh, sk_sm, L.sk[0], B, H, M, D, st));
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sv, sv_sb, sv_sh, sv_sm, L.sv[0], B, H, M, D, st));
+  {
+    const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk[0]};
+    const SlotConv<const void*, float*> cb{sv, sv_sb, sv_sh, sv_sm, L.sv[0]};
+    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+  }
   for (int r = 0; r < rounds; ++r) {
     const bool last = r == rounds - 1;
     SAParams p = sa_params(B, H, N, D, M, qv, L.sk[r], effective_M, causal, scale);
@@ -784,8 +811,11 @@ int murm_murmurate_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
       RUN(C_SEGBR, "seg_attbwd_reduce", launch_seg(dtype, DP, SEG_ATTBWD, s, &G.part, 1, st));
     if (r == 0) {
       const int64_t ssb = (int64_t)H * M * D, ssh = (int64_t)M * D, ssm = D;
-      RUN(C_CONV, "from_state", launch_from_state(slot_dtype, G.Gk, grad_sk, ssb, ssh, ssm, B, H, M, D, st));
-      RUN(C_CONV, "from_state", launch_from_state(slot_dtype, G.Gv, grad_sv, ssb, ssh, ssm, B, H, M, D, st));
+      {
+        const SlotConv<const float*, void*> ca{G.Gk, ssb, ssh, ssm, grad_sk};
+        const SlotConv<const float*, void*> cb{G.Gv, ssb, ssh, ssm, grad_sv};
+        RUN(C_CONV, "from_state", launch_from_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+      }
     }
   }
 

@@ -126,6 +126,17 @@ hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, const Par
 hipError_t launch_du(const DuParams& p, hipStream_t st);
 hipError_t launch_tok_bwd(int dtype, int DP, const TokBwdParams& p, hipStream_t st);
 hipError_t launch_tok_grad(int dtype, int DP, const TokGradParams& p, hipStream_t st);
+template <typename S, typename D>
+struct SlotConv {   // one slot tensor [B,H,M,D] (element strides) <-> fp32 state [BH,M,D]
+  S src;
+  int64_t sb, sh, sm;   // strides of the slot tensor (src for to_state, dst for from_state)
+  D dst;
+};
+// two conversions in one launch (b may be null)
+hipError_t launch_to_state2(int dtype, const SlotConv<const void*, float*>& a,
+                            const SlotConv<const void*, float*>* b, int B, int H, int M, int D, hipStream_t st);
+hipError_t launch_from_state2(int dtype, const SlotConv<const float*, void*>& a,
+                              const SlotConv<const float*, void*>* b, int B, int H, int M, int D, hipStream_t st);
 hipError_t launch_to_state(int dtype, const void* src, int64_t sb, int64_t sh, int64_t sm, float* dst,
                            int B, int H, int M, int D, hipStream_t st);
 hipError_t launch_from_state(int dtype, const float* src, void* dst, int64_t sb, int64_t sh, int64_t sm,

@@ -18,6 +18,8 @@
 //              dW = -(1-a)(K.G'k + V.G'v)/(W+eps)^2.
 // du_kernel: the same EMA backward for the standalone update op.
 
+#include <type_traits>
+
 #include "murm_common.h"
 #include "murm_launch.h"
 
@@ -509,10 +511,12 @@ __global__ __launch_bounds__(256) void du_kernel(DuParams p) {
   }
 }
 
-// fp32 state [BH,M,D] from a [B,H,M,D] slot tensor of any dtype and strides
+// fp32 state [BH,M,D] from a [B,H,M,D] slot tensor of any dtype and strides,
+// and back; blockIdx.y picks one of up to two tensors of one launch.
 template <typename T>
-__global__ void to_state_kernel(const T* __restrict__ src, int64_t sb, int64_t sh, int64_t sm,
-                                float* __restrict__ dst, int B, int H, int M, int D) {
+__global__ void to_state_kernel(SlotConv<const T*, float*> c0, SlotConv<const T*, float*> c1, int B, int H, int M,
+                                int D) {
+  const SlotConv<const T*, float*>& c = blockIdx.y == 0 ? c0 : c1;
   const int64_t total = (int64_t)B * H * M * D;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -522,13 +526,14 @@ __global__ void to_state_kernel(const T* __restrict__ src, int64_t sb, int64_t s
     r /= M;
     const int h = (int)(r % H);
     const int b = (int)(r / H);
-    dst[i] = to_f(src[b * sb + h * sh + m * sm + d]);
+    c.dst[i] = to_f(c.src[b * c.sb + h * c.sh + m * c.sm + d]);
   }
 }
 
 template <typename T>
-__global__ void from_state_kernel(const float* __restrict__ src, T* __restrict__ dst, int64_t sb,
-                                  int64_t sh, int64_t sm, int B, int H, int M, int D) {
+__global__ void from_state_kernel(SlotConv<const float*, T*> c0, SlotConv<const float*, T*> c1, int B, int H,
+                                  int M, int D) {
+  const SlotConv<const float*, T*>& c = blockIdx.y == 0 ? c0 : c1;
   const int64_t total = (int64_t)B * H * M * D;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -538,7 +543,7 @@ __global__ void from_state_kernel(const float* __restrict__ src, T* __restrict__
     r /= M;
     const int h = (int)(r % H);
     const int b = (int)(r / H);
-    dst[b * sb + h * sh + m * sm + d] = from_f<T>(src[i]);
+    c.dst[b * c.sb + h * c.sh + m * c.sm + d] = from_f<T>(c.src[i]);
   }
 }
 
@@ -733,34 +738,55 @@ hipError_t launch_du(const DuParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_to_state(int dtype, const void* src, int64_t sb, int64_t sh, int64_t sm, float* dst,
-                           int B, int H, int M, int D, hipStream_t st) {
-  const int g = grid1d((int64_t)B * H * M * D);
+hipError_t launch_to_state2(int dtype, const SlotConv<const void*, float*>& a,
+                            const SlotConv<const void*, float*>* bp, int B, int H, int M, int D, hipStream_t st) {
+  const dim3 grid(grid1d((int64_t)B * H * M * D), bp ? 2 : 1);
+  const SlotConv<const void*, float*> bb = bp ? *bp : a;
+  auto cv = [](const SlotConv<const void*, float*>& c, auto* tag) {
+    using T = std::remove_const_t<std::remove_pointer_t<decltype(tag)>>;
+    return SlotConv<const T*, float*>{static_cast<const T*>(c.src), c.sb, c.sh, c.sm, c.dst};
+  };
   switch (dtype) {
-    case DT_BF16: hipLaunchKernelGGL((to_state_kernel<__bf16>), dim3(g), dim3(256), 0, st,
-                                     (const __bf16*)src, sb, sh, sm, dst, B, H, M, D); break;
-    case DT_F16: hipLaunchKernelGGL((to_state_kernel<_Float16>), dim3(g), dim3(256), 0, st,
-                                    (const _Float16*)src, sb, sh, sm, dst, B, H, M, D); break;
-    case DT_F32: hipLaunchKernelGGL((to_state_kernel<float>), dim3(g), dim3(256), 0, st,
-                                    (const float*)src, sb, sh, sm, dst, B, H, M, D); break;
+    case DT_BF16: hipLaunchKernelGGL((to_state_kernel<__bf16>), grid, dim3(256), 0, st,
+                                     cv(a, (const __bf16*)nullptr), cv(bb, (const __bf16*)nullptr), B, H, M, D); break;
+    case DT_F16: hipLaunchKernelGGL((to_state_kernel<_Float16>), grid, dim3(256), 0, st,
+                                    cv(a, (const _Float16*)nullptr), cv(bb, (const _Float16*)nullptr), B, H, M, D);
+      break;
+    case DT_F32: hipLaunchKernelGGL((to_state_kernel<float>), grid, dim3(256), 0, st,
+                                    cv(a, (const float*)nullptr), cv(bb, (const float*)nullptr), B, H, M, D); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-hipError_t launch_from_state(int dtype, const float* src, void* dst, int64_t sb, int64_t sh, int64_t sm,
-                             int B, int H, int M, int D, hipStream_t st) {
-  const int g = grid1d((int64_t)B * H * M * D);
+hipError_t launch_from_state2(int dtype, const SlotConv<const float*, void*>& a,
+                              const SlotConv<const float*, void*>* bp, int B, int H, int M, int D, hipStream_t st) {
+  const dim3 grid(grid1d((int64_t)B * H * M * D), bp ? 2 : 1);
+  const SlotConv<const float*, void*> bb = bp ? *bp : a;
+  auto cv = [](const SlotConv<const float*, void*>& c, auto* tag) {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    return SlotConv<const float*, T*>{c.src, c.sb, c.sh, c.sm, static_cast<T*>(c.dst)};
+  };
   switch (dtype) {
-    case DT_BF16: hipLaunchKernelGGL((from_state_kernel<__bf16>), dim3(g), dim3(256), 0, st,
-                                     src, (__bf16*)dst, sb, sh, sm, B, H, M, D); break;
-    case DT_F16: hipLaunchKernelGGL((from_state_kernel<_Float16>), dim3(g), dim3(256), 0, st,
-                                    src, (_Float16*)dst, sb, sh, sm, B, H, M, D); break;
-    case DT_F32: hipLaunchKernelGGL((from_state_kernel<float>), dim3(g), dim3(256), 0, st,
-                                    src, (float*)dst, sb, sh, sm, B, H, M, D); break;
+    case DT_BF16: hipLaunchKernelGGL((from_state_kernel<__bf16>), grid, dim3(256), 0, st,
+                                     cv(a, (__bf16*)nullptr), cv(bb, (__bf16*)nullptr), B, H, M, D); break;
+    case DT_F16: hipLaunchKernelGGL((from_state_kernel<_Float16>), grid, dim3(256), 0, st,
+                                    cv(a, (_Float16*)nullptr), cv(bb, (_Float16*)nullptr), B, H, M, D); break;
+    case DT_F32: hipLaunchKernelGGL((from_state_kernel<float>), grid, dim3(256), 0, st,
+                                    cv(a, (float*)nullptr), cv(bb, (float*)nullptr), B, H, M, D); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_to_state(int dtype, const void* src, int64_t sb, int64_t sh, int64_t sm, float* dst,
+                           int B, int H, int M, int D, hipStream_t st) {
+  return launch_to_state2(dtype, {src, sb, sh, sm, dst}, nullptr, B, H, M, D, st);
+}
+
+hipError_t launch_from_state(int dtype, const float* src, void* dst, int64_t sb, int64_t sh, int64_t sm,
+                             int B, int H, int M, int D, hipStream_t st) {
+  return launch_from_state2(dtype, {src, sb, sh, sm, dst}, nullptr, B, H, M, D, st);
 }
 
 hipError_t launch_idx_pack(const int64_t* src, uint16_t* dst, int64_t rows, int K, int M, hipStream_t st) {
