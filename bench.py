@@ -79,6 +79,20 @@ def byte_model(B, H, N, D, M, R, e):
     return per_launch, flops
 
 
+def call_bytes(B, H, N, D, M, R, e):
+    """Algorithmic HBM bytes of one whole fwd+bwd call (one read of every input
+    and one write of every output per phase, fp32 slot state, int32-sized
+    indices): select+attend 2q+2s+i+w in round 0 and 3q+2s+i+w after it,
+    update+diffuse q+i+w+4s, int64 API indices i; backward per round token side
+    4q+i+w+2s, slot side 2q+i+w+2s, EMA/diffusion 6s, minus the first round's
+    dq read."""
+    T = B * H * N
+    q, s, i, w = T * D * e, B * H * M * D * 4, T * 7 * 4, T * 7 * 4
+    fwd = (2 * q + 2 * s + i + w) + (R - 1) * (3 * q + 2 * s + i + w) + R * (q + i + w + 4 * s) + i
+    bwd = R * ((4 * q + i + w + 2 * s) + (2 * q + i + w + 2 * s) + 6 * s) - q
+    return fwd + bwd
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "slot_murmurate_fwd_bwd_headline_hbm_traffic.md")
 
 
@@ -315,6 +329,14 @@ def main():
         kernels["select_attend"]["score_gemm_TFLOPs"] = round(tf, 2)
         kernels["select_attend"]["mfma_frac"] = round(tf / MFMA_BF16_PEAK_TFLOPS, 4)
     device_ms = sum(ms for ms, _ in kt.values()) / a.steps
+    # the whole call against the HBM floor of its algorithmic bytes (slot_murmurate only)
+    cb = call_bytes(B, H, N, D, M, R, e)
+    t_roof_us = cb / (HBM_PEAK_GBS * 1e9) * 1e6
+    call_roofline = {"bytes": int(cb), "t_roof_us": round(t_roof_us, 2),
+                     "kernel_us_per_step": round(1e3 * device_ms, 2),
+                     "frac_of_kernel_time": round(t_roof_us / (1e3 * device_ms), 4)}
+    if not module:
+        call_roofline["frac_of_step_time"] = round(t_roof_us / (1e3 * ms_per_step), 4)
 
     dname = {"bfloat16": "bf16", "float16": "fp16", "float32": "fp32"}[dt]
     if module:
@@ -335,6 +357,7 @@ def main():
         "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": dname, "data": data, "config": config,
         "roofline": roofline,
+        "call_roofline": call_roofline,
         "kernels": kernels,
         "device_ms_per_step_in_kernels": round(device_ms, 4),
     }
