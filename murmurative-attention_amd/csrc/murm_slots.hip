@@ -283,7 +283,7 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
       const int i = tid + k * nthr, t = i / CW, j = i % CW;
       const bool in = i < SUB * CW && t < cnt && j < KN;
       pw[k] = in ? p.wgt[(row0 + t) * KN + j] : 0.f;
-      pd[k] = (MODE == SEG_ATTBWD && in) ? p.ds_scale * p.ds[(row0 + t) * KN + j] : 0.f;
+      pd[k] = (MODE == SEG_ATTBWD && in) ? p.ds[(row0 + t) * KN + j] : 0.f;  // scaled when stashed
     }
   };
   // registers -> LDS, plus whatever the registers did not cover (small blocks)
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
       const int i = tid + k * nthr;
       if (i < SUB * CW) {
         cw[i] = pw[k];
-        if (MODE == SEG_ATTBWD) cd[i] = pd[k];
+        if (MODE == SEG_ATTBWD) cd[i] = p.ds_scale * pd[k];
       }
     }
     for (int i = tid + 2 * nthr; i < SUB * CW; i += nthr) {
@@ -404,6 +404,308 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
       if (part * DPT + i < p.D) dst[i] = acc[i];
   }
   if (wacc) pp.partW[prow] = accw;
+}
+
+// ---------------------------------------------------------------------------
+// Token-chunk partial sums on MFMA (bf16 / fp16 tokens).
+// The slot sums of a sub-chunk are the product C^T X of the coefficient
+// matrix C [tokens x slots] (at most 7 nonzeros per token: w, or c*ds) and
+// the token rows X [tokens x d].  Per sub-chunk (SUBT tokens) the block stages X
+// transposed (d-major, so 8 consecutive tokens of one dim form one 16-byte
+// MFMA operand) and C^T as hi + lo halves of the token dtype (hi = rn(c),
+// lo = rn(c - hi)); their products with the exact 16-bit X accumulate in
+// fp32, ~2^-16 relative to fp32 coefficients.  The marking threads write the
+// C^T entries and reset them to zero after use, so the table is cleared once
+// per block.  Each vector has its own 4 waves; wave w owns 16-slot tiles
+// w, w+4, ... of the block's slot group and keeps their sums for every dim
+// tile in MFMA accumulators across the chunk; with UPDATE a ones column gives
+// the weight sums.  Fixed
+// k order inside each MFMA and sub-chunks in token order: bitwise
+// reproducible.
+// ---------------------------------------------------------------------------
+constexpr int MMA_WAVES = 4;       // waves per vector
+
+// Byte offset of 16-byte chunk `c` of LDS row `row` (rows of SUBT 16-bit
+// tokens).  The XOR keeps the operand reads of 16 consecutive rows (one chunk
+// each) on 16 distinct 16-byte bank groups; the row >> 4 term spreads the
+// transposed staging stores (rows 8 apart).
+template <int SUBT>
+__device__ __forceinline__ int swz(int row, int c) {
+  constexpr int ROWB = SUBT * 2, CPR = ROWB / 16;
+  const int f = CPR == 8 ? ((row >> 1) ^ (row >> 4)) : ((row >> 2) ^ (row >> 4));
+  return row * ROWB + ((c ^ f) & (CPR - 1)) * 16;
+}
+
+template <int DP, int MODE, int NV, int SUBT>
+struct MmaShape {
+  static constexpr int THREADS = 64 * MMA_WAVES * NV;       // one group of waves per vector
+  static constexpr int DT = DP / 16;                        // dim tiles
+  static constexpr int KINDS = MODE == SEG_ATTBWD ? 2 : 1;  // coefficient kinds (c*ds, w)
+  static constexpr int WTILE = MODE == SEG_UPDATE ? 1 : 0;  // ones tile for the weight sums
+  static constexpr int WT = 256 / DP;                       // slot tiles per wave: 64 accumulators
+  static constexpr int ROWB = SUBT * 2;
+  static constexpr int MS_REG = MMA_WAVES * WT * 16;
+  static constexpr int MS_LDS = (64 * 1024) / (KINDS * 2 * ROWB);  // C^T within 64 KiB
+  static constexpr int MS = MS_REG < MS_LDS ? MS_REG : MS_LDS;    // slots per block
+  static constexpr size_t LDS = (size_t)NV * DP * ROWB + (size_t)KINDS * 2 * MS * ROWB;
+};
+
+template <typename T, int DP, int MODE, int NV, int SUBT>
+__global__ __launch_bounds__(64 * MMA_WAVES * NV, 2) void seg_mma_kernel(SegParams p, PartParams pp) {
+  using V = typename Mfma16<T>::vec;
+  using Sh = MmaShape<DP, MODE, NV, SUBT>;
+  constexpr int DT = Sh::DT, KINDS = Sh::KINDS, WT = Sh::WT, MS = Sh::MS, ROWB = Sh::ROWB;
+  constexpr int MMA_THREADS = Sh::THREADS;
+  constexpr int UPR = DP / 8;                      // 16-byte units per token row
+  constexpr int GROUPS = NV * UPR * (SUBT / 4);    // staging items: (vector, unit, 4 tokens)
+  constexpr int GPT = (GROUPS + MMA_THREADS - 1) / MMA_THREADS;
+  constexpr int TPT = MMA_THREADS / SUBT;          // marking threads per token (one wave)
+  constexpr int JPT = (8 + TPT - 1) / TPT;         // js per marking thread
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* xt = smem;                          // [NV*DP rows][ROWB]
+  unsigned char* ct = smem + NV * DP * ROWB;         // [KINDS][hi, lo][MS rows][ROWB]
+
+  int bh, chunk, sg;
+  const int nsg = (p.M + MS - 1) / MS;
+  part_block(pp.nchunk, nsg, p.B * p.H, bh, chunk, sg);
+  if (bh < 0) return;  // whole block, before any barrier
+  const int b = bh / p.H, h = bh % p.H;
+  const int c_beg = chunk * pp.chunk_tokens;
+  const int c_end = min(p.N, c_beg + pp.chunk_tokens);
+  const int s0 = sg * MS;
+  const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) % MMA_WAVES, vw = (tid >> 6) / MMA_WAVES;
+  const int ms_here = min(MS, p.M - s0);
+  const int ntiles = (ms_here + 15) / 16;
+
+  for (int i = tid; i < KINDS * 2 * MS * ROWB / 16; i += MMA_THREADS)
+    reinterpret_cast<uint4*>(ct)[i] = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();  // cleared before any marking store
+
+  // ---- prefetch registers: token rows, then (marking) one index row and the
+  // coefficients of this thread's js
+  uint4 px[GPT][4];
+  uint4 pidx;
+  float pc[KINDS][JPT];
+  const int mt = tid / TPT, mk = tid % TPT;  // marking token, j group
+  // Prefetch: loads from clamped (always valid) rows straight into the
+  // registers, validity applied when staging, so no load is predicated or
+  // copied (either makes the wave wait for it before the products).
+  const bool wide = p.va.vec && (NV == 1 || p.vb.vec) && (p.D & 7) == 0;
+  auto unit_of = [&](int item, int& v, int& u, int& g4) {
+    v = item / (UPR * (SUBT / 4));
+    const int rem = item % (UPR * (SUBT / 4));
+    u = rem % UPR;
+    g4 = rem / UPR;
+  };
+  auto fetch = [&](int n0) {
+    // marking loads first, token rows last (nothing after them touches a register)
+    const int64_t row = (int64_t)bh * p.N + min(n0 + mt, p.N - 1);
+    pidx = *reinterpret_cast<const uint4*>(p.idx + row * IDX_ROW);
+#pragma unroll
+    for (int q = 0; q < JPT; ++q) {
+      const int j = min(JPT * mk + q, KN - 1);
+      if (MODE == SEG_ATTBWD) {
+        pc[0][q] = p.ds[row * KN + j];  // scaled when marked
+        pc[KINDS - 1][q] = p.wgt[row * KN + j];
+      } else {
+        pc[0][q] = p.wgt[row * KN + j];
+      }
+    }
+    if (wide) {
+#pragma unroll
+      for (int g = 0; g < GPT; ++g) {
+        const int item = tid + g * MMA_THREADS;
+        if (GROUPS % MMA_THREADS != 0 && item >= GROUPS) continue;
+        int v, u, g4;
+        unit_of(item, v, u, g4);
+        const TokView& tv = v == 0 ? p.va : p.vb;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          px[g][k] = *reinterpret_cast<const uint4*>(tok_row<T>(tv, b, h, min(n0 + 4 * g4 + k, p.N - 1)) + u * 8);
+      }
+    }
+  };
+
+  // ---- staging: 4 tokens x 8 dims transposed into 8 dim rows of 4 tokens
+  auto stash = [&](int n0) {
+    const int cnt = min(SUBT, c_end - n0);
+#pragma unroll
+    for (int g = 0; g < GPT; ++g) {
+      const int item = tid + g * MMA_THREADS;
+      if (item >= GROUPS) continue;
+      int v, u, g4;
+      unit_of(item, v, u, g4);
+      uint4 x[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int t = 4 * g4 + k;
+        const bool ok = t < cnt && u * 8 < p.D;
+        if (wide) {
+          x[k] = px[g][k];
+        } else {  // unaligned rows or a ragged last unit: element loads now, packed as dwords
+          const uint16_t* e =
+              reinterpret_cast<const uint16_t*>(tok_row<T>(v == 0 ? p.va : p.vb, b, h, min(n0 + t, p.N - 1))) + u * 8;
+          uint32_t w[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = u * 8 + 2 * q < p.D ? e[2 * q] : 0u;
+            const uint32_t hi = u * 8 + 2 * q + 1 < p.D ? e[2 * q + 1] : 0u;
+            w[q] = lo | (hi << 16);
+          }
+          x[k] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        if (!ok) x[k] = make_uint4(0u, 0u, 0u, 0u);
+      }
+      const uint32_t* x0 = reinterpret_cast<const uint32_t*>(&x[0]);
+      const uint32_t* x1 = reinterpret_cast<const uint32_t*>(&x[1]);
+      const uint32_t* x2 = reinterpret_cast<const uint32_t*>(&x[2]);
+      const uint32_t* x3 = reinterpret_cast<const uint32_t*>(&x[3]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
+        uint2 o;
+        o.x = __builtin_amdgcn_perm(x1[i >> 1], x0[i >> 1], sel);
+        o.y = __builtin_amdgcn_perm(x3[i >> 1], x2[i >> 1], sel);
+        const int r = v * DP + u * 8 + i;
+        *reinterpret_cast<uint2*>(xt + swz<SUBT>(r, g4 >> 1) + (g4 & 1) * 8) = o;
+      }
+    }
+  };
+
+  // ---- marking: entries of token mt for its js (first j of a slot; later
+  // js naming the same slot add their coefficients in j order)
+  int prev[JPT];
+#pragma unroll
+  for (int q = 0; q < JPT; ++q) prev[q] = -1;
+  auto put = [&](int off, int kind, float c) {
+    const T hi = (T)c;
+    const T lo = (T)(c - (float)hi);
+    *reinterpret_cast<T*>(ct + (kind * 2 + 0) * MS * ROWB + off) = hi;
+    *reinterpret_cast<T*>(ct + (kind * 2 + 1) * MS * ROWB + off) = lo;
+  };
+  auto mark = [&](int n0) {
+    // clear this thread's entries of the previous sub-chunk first (the
+    // threads of one token are one wave, so these stores precede its new ones)
+#pragma unroll
+    for (int q = 0; q < JPT; ++q)
+      if (prev[q] >= 0)
+#pragma unroll
+        for (int kind = 0; kind < KINDS; ++kind) put(prev[q], kind, 0.f);
+    const bool live = n0 + mt < c_end;
+    const uint4 ir = live ? pidx : make_uint4(~0u, ~0u, ~0u, ~0u);
+    const int64_t row = (int64_t)bh * p.N + n0 + mt;
+#pragma unroll
+    for (int q = 0; q < JPT; ++q) {
+      prev[q] = -1;
+      const int j = JPT * mk + q;
+      if (j >= KN) continue;
+      const uint32_t sj = idx_at(ir, j);
+      const uint32_t sl = sj - (uint32_t)s0;  // slots of this group; others wrap past MS
+      if (sl >= (uint32_t)MS || sj >= (uint32_t)p.M) continue;
+      uint32_t before = 0, after = 0;
+#pragma unroll
+      for (int x = 0; x < KN; ++x) {
+        const uint32_t hit = idx_at(ir, x) == sj ? 1u : 0u;
+        before |= (x < j ? hit : 0u) << x;
+        after |= (x > j ? hit : 0u) << x;
+      }
+      if (before) continue;
+      float c[KINDS];
+#pragma unroll
+      for (int kind = 0; kind < KINDS; ++kind) c[kind] = pc[kind][q];
+      if (MODE == SEG_ATTBWD) c[0] *= p.ds_scale;
+      for (uint32_t r = after; r; r &= r - 1u) {  // caller-given duplicate indices only
+        const int x = __builtin_ctz(r);
+        if (MODE == SEG_ATTBWD) {
+          c[0] += p.ds_scale * p.ds[row * KN + x];
+          c[KINDS - 1] += p.wgt[row * KN + x];
+        } else {
+          c[0] += p.wgt[row * KN + x];
+        }
+      }
+      const int off = swz<SUBT>((int)sl, mt >> 3) + (mt & 7) * 2;
+#pragma unroll
+      for (int kind = 0; kind < KINDS; ++kind) put(off, kind, c[kind]);
+      prev[q] = off;
+    }
+  };
+
+  // wave group vw owns vector vw (coefficient kind vw with ATTBWD)
+  const int kind = MODE == SEG_ATTBWD ? vw : 0;
+  const bool wsum = Sh::WTILE && vw == 0;
+  f32x4 acc[WT][DT];
+  f32x4 accw[Sh::WTILE ? WT : 1];
+#pragma unroll
+  for (int i = 0; i < WT; ++i) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[i][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (Sh::WTILE) accw[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  V ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (T)((lane & 15) == 0 ? 1.f : 0.f);
+  auto load_a = [&](int tile, int chk, V (&a)[2]) {
+    const int srow = tile * 16 + (lane & 15);
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+      a[hl] = *reinterpret_cast<const V*>(ct + (kind * 2 + hl) * MS * ROWB + swz<SUBT>(srow, chk));
+  };
+
+  fetch(c_beg);
+  for (int n0 = c_beg; n0 < c_end; n0 += SUBT) {
+    stash(n0);
+    mark(n0);
+    __syncthreads();
+    if (n0 + SUBT < c_end) fetch(n0 + SUBT);  // in flight during the products
+#pragma unroll
+    for (int ks = 0; ks < SUBT / 32; ++ks) {
+      const int chk = ks * 4 + (lane >> 4);
+      V bx[DT];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        bx[dt] = *reinterpret_cast<const V*>(xt + swz<SUBT>(vw * DP + dt * 16 + (lane & 15), chk));
+      V a[2], an[2];
+      if (wave < ntiles) load_a(wave, chk, a);
+#pragma unroll
+      for (int i = 0; i < WT; ++i) {
+        const int tile = wave + MMA_WAVES * i;
+        if (tile >= ntiles) break;  // wave-uniform
+        if (i + 1 < WT && tile + MMA_WAVES < ntiles) load_a(tile + MMA_WAVES, chk, an);  // next tile in flight
+        // lo halves of every accumulator, then hi halves
+#pragma unroll
+        for (int hl = 1; hl >= 0; --hl) {
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) acc[i][dt] = mfma_16x16x32(a[hl], bx[dt], acc[i][dt]);
+          if (Sh::WTILE && wsum) accw[i] = mfma_16x16x32(a[hl], ones, accw[i]);
+        }
+        a[0] = an[0];
+        a[1] = an[1];
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- partial sums: lane holds rows 4*(lane>>4)+r of column lane&15 per tile
+  const int64_t prow0 = ((int64_t)chunk * p.B * p.H + bh) * p.M;
+  float* dst0 = (vw == 0 ? pp.partA : pp.partB);
+#pragma unroll
+  for (int i = 0; i < WT; ++i) {
+    const int tile = wave + MMA_WAVES * i;
+    if (tile >= ntiles) break;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int slot = s0 + tile * 16 + 4 * (lane >> 4) + r;
+      if (slot >= p.M) continue;
+      const int64_t prow = prow0 + slot;
+      float* dst = dst0 + prow * p.D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = dt * 16 + (lane & 15);
+        if (d < p.D) dst[d] = acc[i][dt][r];
+      }
+      if (wsum && (lane & 15) == 0) pp.partW[prow] = accw[i][r];
+    }
+  }
 }
 
 template <int DP, int MODE>
@@ -662,16 +964,44 @@ bool part_ok(const SegParams& p, int mode, const PartParams* pp, int& nvec, int&
   return pp && pp->nchunk > 0 && lds <= 160 * 1024;
 }
 
+constexpr int MSUBT = 32;   // tokens per sub-chunk of the MFMA kernel
+
+template <typename T, int DP, int MODE, int NV>
+hipError_t launch_mma(const SegParams& p, const PartParams& pp, int stage, hipStream_t st) {
+  using Sh = MmaShape<DP, MODE, NV, MSUBT>;
+  const int BH = p.B * p.H;
+  if (stage == 0) {
+    const void* fn = reinterpret_cast<const void*>(&seg_mma_kernel<T, DP, MODE, NV, MSUBT>);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Sh::LDS);
+    if (e != hipSuccess) return e;
+    const int nsg = (p.M + Sh::MS - 1) / Sh::MS;
+    dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk * nsg);
+    hipLaunchKernelGGL((seg_mma_kernel<T, DP, MODE, NV, MSUBT>), grid, dim3(Sh::THREADS), Sh::LDS, st, p, pp);
+  } else {
+    const int G = (p.M + GS - 1) / GS;
+    hipLaunchKernelGGL((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G),
+                       dim3(red_threads(pp.nchunk, DP)), 0, st, p, pp);
+  }
+  return hipGetLastError();
+}
+
 // stage 0: the partial-sum kernel; stage 1: the chunk reduction with the epilogue.
 template <typename T, int DP>
 hipError_t launch_seg_t(const SegParams& p, int mode, const PartParams* pp, int stage, hipStream_t st) {
-  int nvec, MS;
-  size_t lds;
-  if (part_ok<T, DP>(p, mode, pp, nvec, MS, lds)) {
-    if (mode == SEG_UPDATE) return launch_part<T, DP, SEG_UPDATE>(p, *pp, nvec, MS, lds, stage, st);
-    return launch_part<T, DP, SEG_ATTBWD>(p, *pp, nvec, MS, lds, stage, st);
+  if constexpr (sizeof(T) == 2) {
+    if (!pp || pp->nchunk <= 0 || pp->chunk_tokens % MSUBT != 0) return hipErrorInvalidValue;
+    if (mode == SEG_ATTBWD) return launch_mma<T, DP, SEG_ATTBWD, 2>(p, *pp, stage, st);
+    if (p.b_same_as_a) return launch_mma<T, DP, SEG_UPDATE, 1>(p, *pp, stage, st);
+    return launch_mma<T, DP, SEG_UPDATE, 2>(p, *pp, stage, st);
+  } else {
+    int nvec, MS;
+    size_t lds;
+    if (part_ok<T, DP>(p, mode, pp, nvec, MS, lds)) {
+      if (mode == SEG_UPDATE) return launch_part<T, DP, SEG_UPDATE>(p, *pp, nvec, MS, lds, stage, st);
+      return launch_part<T, DP, SEG_ATTBWD>(p, *pp, nvec, MS, lds, stage, st);
+    }
+    return hipErrorInvalidValue;  // no chunk scratch carved
   }
-  return hipErrorInvalidValue;  // no chunk scratch carved, or d > 128
 }
 
 inline int grid1d(int64_t n, int tpb = 256) {
@@ -682,22 +1012,8 @@ inline int grid1d(int64_t n, int tpb = 256) {
 }  // namespace
 
 bool seg_two_stage(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp) {
-  int nvec, MS;
-  size_t lds;
-#define MURM_SEGQ(T)                                                   \
-  switch (DP) {                                                        \
-    case 32: return part_ok<T, 32>(p, mode, pp, nvec, MS, lds);        \
-    case 64: return part_ok<T, 64>(p, mode, pp, nvec, MS, lds);        \
-    case 128: return part_ok<T, 128>(p, mode, pp, nvec, MS, lds);      \
-    default: return false;                                             \
-  }
-  switch (dtype) {
-    case DT_BF16: MURM_SEGQ(__bf16)
-    case DT_F16: MURM_SEGQ(_Float16)
-    case DT_F32: MURM_SEGQ(float)
-    default: return false;
-  }
-#undef MURM_SEGQ
+  (void)dtype; (void)DP; (void)mode; (void)p;
+  return pp && pp->nchunk > 0;  // every served shape fits the token-chunk kernels
 }
 
 int seg_chunks(int B, int H, int N, int M, int D) {
