@@ -143,9 +143,9 @@ struct Carve {
 };
 
 // token-chunk partial sums of the slot reductions (shared by every round)
-PartParams carve_parts(Carve& c, int B, int H, int N, int D, int M) {
+PartParams carve_parts(Carve& c, int B, int H, int N, int D, int M, int mode) {
   PartParams pp{};
-  pp.nchunk = seg_chunks(B, H, N, M, D);
+  pp.nchunk = seg_chunks(B, H, N, M, D, mode);
   if (pp.nchunk <= 0) return pp;
   pp.chunk_tokens = seg_chunk_tokens(N, pp.nchunk);
   const size_t BH = (size_t)B * H, S = BH * M * D;
@@ -181,7 +181,7 @@ FwdLayout fwd_layout(void* ws, int B, int H, int N, int D, int M, int R, int sha
       L.w[r] = c.take<float>(BH * N * KN);
     }
   }
-  if (R > 1) L.part = carve_parts(c, B, H, N, D, M);
+  if (R > 1) L.part = carve_parts(c, B, H, N, D, M, SEG_UPDATE);
   L.bytes = c.off;
   return L;
 }
@@ -213,7 +213,7 @@ BwdLayout bwd_layout(void* ws, int B, int H, int N, int D, int M, int R, int sha
     L.ck[i] = c.take<float>(S);
     L.cv[i] = c.take<float>(S);
   }
-  L.part = carve_parts(c, B, H, N, D, M);
+  L.part = carve_parts(c, B, H, N, D, M, SEG_ATTBWD);
   L.bytes = c.off;
   return L;
 }
@@ -242,7 +242,7 @@ OpLayout op_layout(void* ws, int B, int H, int N, int D, int M, int kind) {
     L.dk = c.take<float>(S); L.dv = c.take<float>(S); L.dW = c.take<float>(BH * M);
     L.ck = c.take<float>(S); L.cv = c.take<float>(S);
   }
-  if (kind != 0) L.part = carve_parts(c, B, H, N, D, M);
+  if (kind != 0) L.part = carve_parts(c, B, H, N, D, M, kind == 1 ? SEG_ATTBWD : SEG_UPDATE);
   L.bytes = c.off;
   return L;
 }

@@ -116,7 +116,7 @@ size_t sa_lds_bytes(int dtype, int DP, int M);
 hipError_t launch_attend_idx(int dtype, int DP, const AttendIdxParams& p, hipStream_t st);
 hipError_t launch_select_attend(int dtype, int DP, const SAParams& p, hipStream_t st);
 hipError_t launch_gather_out(int dtype, int DP, const OutParams& p, hipStream_t st);
-int seg_chunks(int B, int H, int N, int M, int D);   // 0: shape not served (d > 128)
+int seg_chunks(int B, int H, int N, int M, int D, int mode);   // 0: shape not served (d > 128)
 int seg_chunk_tokens(int N, int nchunk);
 // stage 0: token-chunk partial sums; stage 1: chunk reduction + epilogue.
 // seg_two_stage() is false when no chunk scratch was carved (launch_seg fails then).

@@ -190,7 +190,8 @@ __device__ void attbwd_epilogue(const SegParams& p, int bh, int g0, int halo, in
 // ---------------------------------------------------------------------------
 constexpr int SUB = 128;    // tokens per staged sub-chunk
 constexpr int CW = 8;       // coefficient row (7 used)
-constexpr int NCMAX = 16;   // chunks per (b,h)
+constexpr int NCMAX = 32;   // chunks per (b,h)
+constexpr int NCB = 16;     // chunk partials loaded together by the reduction
 // reduction threads: with many chunks every (vector, row, 4 dims) item of a
 // group gets its own thread (up to 1024), so all chunk loads are in flight at
 // once; with few chunks (many heads) 256-thread blocks keep more groups resident
@@ -727,14 +728,17 @@ __global__ __launch_bounds__(RED_THREADS) void seg_reduce_kernel(SegParams p, Pa
     if (m >= 0 && m < p.M && d < p.D) {
       const float* src = (v == 0 ? pp.partA : pp.partB) + ((int64_t)bh * p.M + m) * p.D + d;
       if ((p.D & 3) == 0) {
-        float4 x[NCMAX];
+        for (int c0 = 0; c0 < nc; c0 += NCB) {  // chunk order: batches of NCB loads in flight
+          float4 x[NCB];
 #pragma unroll
-        for (int c = 0; c < NCMAX; ++c)
-          x[c] = c < nc ? *reinterpret_cast<const float4*>(src + c * cstride) : make_float4(0.f, 0.f, 0.f, 0.f);
+          for (int c = 0; c < NCB; ++c)
+            x[c] = c0 + c < nc ? *reinterpret_cast<const float4*>(src + (c0 + c) * cstride)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int c = 0; c < NCMAX; ++c) {
-          if (c < nc) {
-            sum.x += x[c].x; sum.y += x[c].y; sum.z += x[c].z; sum.w += x[c].w;
+          for (int c = 0; c < NCB; ++c) {
+            if (c0 + c < nc) {
+              sum.x += x[c].x; sum.y += x[c].y; sum.z += x[c].z; sum.w += x[c].w;
+            }
           }
         }
       } else {
@@ -1016,12 +1020,18 @@ bool seg_two_stage(int dtype, int DP, int mode, const SegParams& p, const PartPa
   return pp && pp->nchunk > 0;  // every served shape fits the token-chunk kernels
 }
 
-int seg_chunks(int B, int H, int N, int M, int D) {
-  // token-chunk path: about 256 (b,h,chunk) blocks of whole sub-chunks, at most NCMAX per (b,h)
+int seg_chunks(int B, int H, int N, int M, int D, int mode) {
+  // token-chunk path, whole sub-chunks, at most NCMAX per (b,h): about 512
+  // (b,h,chunk,slot group) blocks for the update (two one-vector blocks fit a
+  // CU; a 16-bit update block holds 16384/d slots), about 256 (b,h,chunk)
+  // blocks for the attend backward (one two-vector block per CU by registers)
   if (D > 128 || M < 1) return 0;
   const int BH = B * H;
   const int per = (N + SUB - 1) / SUB;
-  int c = (256 + BH - 1) / BH;
+  const int DP = D <= 32 ? 32 : (D <= 64 ? 64 : 128);
+  const int nsg = (M + 16384 / DP - 1) / (16384 / DP);
+  const int target = mode == SEG_UPDATE ? (512 + nsg - 1) / nsg : 256;
+  int c = (target + BH - 1) / BH;
   if (c > NCMAX) c = NCMAX;
   return c < 1 ? 1 : (c > per ? per : c);
 }
