@@ -232,18 +232,25 @@ __device__ __forceinline__ void stage_table(float* __restrict__ dst, const float
   }
 }
 
-// 8 raw token elements (one or two 16-byte units), so loads for many tokens
-// can be in flight before any is converted
+// 8 raw token elements row[d0 ..] (one or two 16-byte units), so loads for
+// many tokens can be in flight before any is converted.  WIDE (rows 16-byte
+// aligned and D % 8 == 0, decided per launch) takes one unconditional 16-byte
+// load per unit straight into the result registers (lanes with d0 >= D
+// re-read unit 0; unraw8 zeroes them).  Otherwise the elements are loaded one
+// by one.  The two paths are separate kernel instances: a result that may
+// come from either makes the compiler wait for the wide load at once.
 template <typename T>
 struct Raw8 {
   uint4 u[sizeof(T) / 2];
 };
-template <typename T>
-__device__ __forceinline__ Raw8<T> raw8(const T* __restrict__ row, int d0, int D, bool vec) {
+template <typename T, bool WIDE>
+__device__ __forceinline__ Raw8<T> raw8(const T* __restrict__ row, int d0, int D) {
   Raw8<T> r;
-  if (vec && d0 + 8 <= D) {
+  if constexpr (WIDE) {
+    const int dd = d0 < D ? d0 : 0;
 #pragma unroll
-    for (int k = 0; k < (int)(sizeof(T) / 2); ++k) r.u[k] = *reinterpret_cast<const uint4*>(row + d0 + k * (16 / sizeof(T)));
+    for (int k = 0; k < (int)(sizeof(T) / 2); ++k)
+      r.u[k] = *reinterpret_cast<const uint4*>(row + dd + k * (16 / (int)sizeof(T)));
   } else {
     T* e = reinterpret_cast<T*>(&r);
 #pragma unroll
@@ -252,10 +259,10 @@ __device__ __forceinline__ Raw8<T> raw8(const T* __restrict__ row, int d0, int D
   return r;
 }
 template <typename T>
-__device__ __forceinline__ void unraw8(const Raw8<T>& r, float (&o)[8]) {
+__device__ __forceinline__ void unraw8(const Raw8<T>& r, float (&o)[8], bool live = true) {
   const T* e = reinterpret_cast<const T*>(&r);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = to_f(e[i]);
+  for (int i = 0; i < 8; ++i) o[i] = live ? to_f(e[i]) : 0.f;
 }
 
 // 8 floats of a staged table row (16-byte aligned: d0 % 8 == 0)

@@ -436,7 +436,7 @@ __global__ __launch_bounds__(256) void gather_out_kernel(OutParams p) {
 constexpr int GO_THREADS = 512;
 constexpr int GO_PASSES = 8;
 
-template <typename T, int DP>
+template <typename T, int DP, bool WIDE>
 __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p, int nchunk) {
   constexpr int DCH = DP / 8, TPP = GO_THREADS / DCH, RSD = DP + 4;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -447,15 +447,20 @@ __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p,
   const int dc = threadIdx.x % DCH, d0 = dc * 8;
   const int c_beg = chunk * GO_PASSES * TPP;
   float acc[GO_PASSES][8];
+  if (p.base.p) {  // every pass's residual row in flight before any is converted
+    Raw8<T> rb[GO_PASSES];
 #pragma unroll
-  for (int q = 0; q < GO_PASSES; ++q) {
-    const int n = c_beg + q * TPP + threadIdx.x / DCH;
-    if (p.base.p && n < p.N) {
-      load8<T>(tok_row<T>(p.base, b, h, n), d0, p.D, p.base.vec, acc[q]);
-    } else {
+    for (int q = 0; q < GO_PASSES; ++q)
+      rb[q] = raw8<T, WIDE>(tok_row<T>(p.base, b, h, min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1)), d0,
+                            p.D);
+#pragma unroll
+    for (int q = 0; q < GO_PASSES; ++q)
+      unraw8<T>(rb[q], acc[q], d0 < p.D && c_beg + q * TPP + (int)threadIdx.x / DCH < p.N);
+  } else {
+#pragma unroll
+    for (int q = 0; q < GO_PASSES; ++q)
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[q][i] = 0.f;
-    }
   }
   for (int r = 0; r < p.R; ++r) {
     // the round's index rows and weights of every pass are requested before
@@ -523,11 +528,16 @@ hipError_t launch_out_t(const OutParams& p, hipStream_t st) {
     constexpr int TPP = GO_THREADS / (DP / 8);
     const int BH = p.B * p.H;
     const int nchunk = (p.N + GO_PASSES * TPP - 1) / (GO_PASSES * TPP);
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_out_lds_kernel<T, DP>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const bool wide = (!p.base.p || p.base.vec) && p.D % 8 == 0;
+    const void* fn = wide ? reinterpret_cast<const void*>(&gather_out_lds_kernel<T, DP, true>)
+                          : reinterpret_cast<const void*>(&gather_out_lds_kernel<T, DP, false>);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
-    hipLaunchKernelGGL((gather_out_lds_kernel<T, DP>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
+    if (wide)
+      hipLaunchKernelGGL((gather_out_lds_kernel<T, DP, true>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
+    else
+      hipLaunchKernelGGL((gather_out_lds_kernel<T, DP, false>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
     return hipGetLastError();
   }
   constexpr int TPB = 256 / (DP / 8);

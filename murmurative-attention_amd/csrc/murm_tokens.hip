@@ -13,6 +13,8 @@
 // Deferring these to one pass after the slot chain writes each token
 // gradient once instead of read-modify-writing it every round.
 
+#include <initializer_list>
+
 #include "murm_common.h"
 #include "murm_launch.h"
 
@@ -169,7 +171,7 @@ struct TokShape {
   static constexpr int RSD = DP + 4;                   // staged row stride
 };
 
-template <typename T, int DP, int NP, bool HV>
+template <typename T, int DP, int NP, bool HV, bool WIDE>
 __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams p, int nchunk) {
   using S = TokShape<DP>;
   constexpr int DCH = S::DCH, TPP = S::TPP, RSD = S::RSD;
@@ -186,14 +188,19 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
   uint4 ix[NP];
   Raw8<T> rg[NP], rk[NP], rv[HV ? NP : 1];
   float wq[NP][JPL], gq[NP][JPL];
+  // token rows are loaded unconditionally (an absent view reads a present
+  // one and is ignored): a load under the same condition as its use would be
+  // merged with the conversion and waited for at once
+  const TokView& vg = p.g.p ? p.g : p.tk;
+  const TokView& vk = p.tk.p ? p.tk : p.g;
 #pragma unroll
   for (int q = 0; q < NP; ++q) {
     const int n = min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1);
     const int64_t row = (int64_t)bh * p.N + n;
     ix[q] = *reinterpret_cast<const uint4*>(p.idx + row * IDX_ROW);
-    if (has_g) rg[q] = raw8<T>(tok_row<T>(p.g, b, h, n), d0, p.D, p.g.vec);
-    if (has_k) rk[q] = raw8<T>(tok_row<T>(p.tk, b, h, n), d0, p.D, p.tk.vec);
-    if constexpr (HV) rv[q] = raw8<T>(tok_row<T>(p.tv, b, h, n), d0, p.D, p.tv.vec);
+    rg[q] = raw8<T, WIDE>(tok_row<T>(vg, b, h, n), d0, p.D);
+    rk[q] = raw8<T, WIDE>(tok_row<T>(vk, b, h, n), d0, p.D);
+    if constexpr (HV) rv[q] = raw8<T, WIDE>(tok_row<T>(p.tv, b, h, n), d0, p.D);
 #pragma unroll
     for (int u = 0; u < JPL; ++u) {
       const int j = dc + u * DCH;
@@ -219,9 +226,9 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
     const uint32_t sl[KN] = {ir.x & 0xFFFF, ir.x >> 16, ir.y & 0xFFFF, ir.y >> 16,
                              ir.z & 0xFFFF, ir.z >> 16, ir.w & 0xFFFF};
     float g[8], a[8], c[8];
-    if (has_g) unraw8<T>(rg[q], g);
-    if (has_k) unraw8<T>(rk[q], a);
-    if constexpr (HV) unraw8<T>(rv[q], c);
+    if (has_g) unraw8<T>(rg[q], g, d0 < p.D);
+    if (has_k) unraw8<T>(rk[q], a, d0 < p.D);
+    if constexpr (HV) unraw8<T>(rv[q], c, d0 < p.D);
     float dw[KN];
 #pragma unroll
     for (int j = 0; j < KN; ++j) {
@@ -275,7 +282,7 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
 
 // tok_grad with each round's tables staged in LDS in turn; a thread keeps the
 // gradients of its PASSES tokens in registers across the rounds.
-template <typename T, int DP, int PASSES, bool KV>
+template <typename T, int DP, int PASSES, bool KV, bool WIDE>
 __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParams p, int nchunk) {
   using S = TokShape<DP>;
   constexpr int DCH = S::DCH, TPP = S::TPP, RSD = S::RSD;
@@ -289,15 +296,19 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParam
   const int c_beg = chunk * PASSES * TPP;
   constexpr int PK = KV ? PASSES : 1;  // token-key / token-value gradients (legacy form only)
   float aq[PASSES][8], ak[PK][8], av[PK][8];
+  if (p.g.p) {  // every pass's residual row in flight before any is converted
+    Raw8<T> rg[PASSES];
 #pragma unroll
-  for (int q = 0; q < PASSES; ++q) {
-    const int n = c_beg + q * TPP + threadIdx.x / DCH;
-    if (p.g.p && n < p.N) {
-      load8<T>(tok_row<T>(p.g, b, h, n), d0, p.D, p.g.vec, aq[q]);
-    } else {
+    for (int q = 0; q < PASSES; ++q)
+      rg[q] = raw8<T, WIDE>(tok_row<T>(p.g, b, h, min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1)), d0, p.D);
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q)
+      unraw8<T>(rg[q], aq[q], d0 < p.D && c_beg + q * TPP + (int)threadIdx.x / DCH < p.N);
+  } else {
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q)
 #pragma unroll
       for (int i = 0; i < 8; ++i) aq[q][i] = 0.f;
-    }
   }
 #pragma unroll
   for (int q = 0; q < PK; ++q)
@@ -434,18 +445,32 @@ inline bool tables_fit(int nt, int M, int DP) {
   return (size_t)nt * M * (DP + 4) * 4 + (size_t)M * 4 <= 150 * 1024;
 }
 
-template <typename T, int DP, int NP, bool HV>
-hipError_t launch_tok_bwd_lds(const TokBwdParams& p, int nt, hipStream_t st) {
+// 16-byte token loads for every row the kernel reads (see raw8)
+inline bool wide_rows(std::initializer_list<const TokView*> views, int D) {
+  if (D % 8 != 0) return false;
+  for (const TokView* v : views)
+    if (v->p && !v->vec) return false;
+  return true;
+}
+
+template <typename T, int DP, int NP, bool HV, bool WIDE>
+hipError_t launch_tok_bwd_lds_w(const TokBwdParams& p, int nt, hipStream_t st) {
   using S = TokShape<DP>;
   const int BH = p.B * p.H;
   const int nchunk = (p.N + NP * S::TPP - 1) / (NP * S::TPP);
   const size_t lds = (size_t)nt * p.M * S::RSD * 4 + (size_t)p.M * 4;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&tok_bwd_lds_kernel<T, DP, NP, HV>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&tok_bwd_lds_kernel<T, DP, NP, HV, WIDE>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
-  hipLaunchKernelGGL((tok_bwd_lds_kernel<T, DP, NP, HV>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
+  hipLaunchKernelGGL((tok_bwd_lds_kernel<T, DP, NP, HV, WIDE>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
   return hipGetLastError();
+}
+
+template <typename T, int DP, int NP, bool HV>
+hipError_t launch_tok_bwd_lds(const TokBwdParams& p, int nt, hipStream_t st) {
+  if (wide_rows({&p.g, &p.tk, &p.tv}, p.D)) return launch_tok_bwd_lds_w<T, DP, NP, HV, true>(p, nt, st);
+  return launch_tok_bwd_lds_w<T, DP, NP, HV, false>(p, nt, st);
 }
 
 template <typename T, int DP>
@@ -464,18 +489,24 @@ hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <typename T, int DP, int PASSES, bool KV>
-hipError_t launch_tok_grad_lds(const TokGradParams& p, int nt, hipStream_t st) {
+template <typename T, int DP, int PASSES, bool KV, bool WIDE>
+hipError_t launch_tok_grad_lds_w(const TokGradParams& p, int nt, hipStream_t st) {
   using S = TokShape<DP>;
   const int BH = p.B * p.H;
   const int nchunk = (p.N + PASSES * S::TPP - 1) / (PASSES * S::TPP);
   const size_t lds = (size_t)nt * p.M * S::RSD * 4;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&tok_grad_lds_kernel<T, DP, PASSES, KV>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&tok_grad_lds_kernel<T, DP, PASSES, KV, WIDE>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
-  hipLaunchKernelGGL((tok_grad_lds_kernel<T, DP, PASSES, KV>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
+  hipLaunchKernelGGL((tok_grad_lds_kernel<T, DP, PASSES, KV, WIDE>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
   return hipGetLastError();
+}
+
+template <typename T, int DP, int PASSES, bool KV>
+hipError_t launch_tok_grad_lds(const TokGradParams& p, int nt, hipStream_t st) {
+  if (wide_rows({&p.g}, p.D)) return launch_tok_grad_lds_w<T, DP, PASSES, KV, true>(p, nt, st);
+  return launch_tok_grad_lds_w<T, DP, PASSES, KV, false>(p, nt, st);
 }
 
 template <typename T, int DP>
