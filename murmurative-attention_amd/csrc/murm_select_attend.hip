@@ -25,11 +25,13 @@ namespace murm {
 
 namespace {
 
-template <int DP> struct SAShape {
+template <int DP, int WAVES_ = 4> struct SAShape {
   static constexpr int G = (DP <= 64) ? 4 : 2;   // 16-token groups per wave
-  static constexpr int WAVES = 4;
+  static constexpr int WAVES = WAVES_;
   static constexpr int TOK = WAVES * G * 16;     // tokens per block
 };
+// 16-bit kernel: 8 waves share one staging of the head's keys (one block per CU)
+constexpr int SA16_WAVES = 8;
 
 // mask / bias / causal / effective_M slow path for one score
 __device__ __forceinline__ float masked_key(const SAParams& p, int b, int h, int n, int m,
@@ -108,7 +110,7 @@ __device__ __forceinline__ V load_operand8(const T* row, int d0, int D, bool vec
 // 16-bit tokens (bf16 / fp16): hi/lo split keys in LDS, 16x16x32 MFMA
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ __launch_bounds__(256) void sa_kernel16(SAParams p) {
+__global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
   using V = typename Mfma16<T>::vec;
   constexpr int G = SAShape<DP>::G;
   constexpr int KC = DP / 32;
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(256) void sa_kernel16(SAParams p) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int quad = lane >> 4, col = lane & 15;
-  const int tok0 = blockIdx.x * SAShape<DP>::TOK + wave * (G * 16);
+  const int tok0 = blockIdx.x * SAShape<DP, SA16_WAVES>::TOK + wave * (G * 16);
   if (tok0 >= p.N) return;  // whole wave past the end (no block-wide sync below)
 
   V bq[G][KC];
@@ -210,17 +212,25 @@ __global__ __launch_bounds__(256) void sa_kernel16(SAParams p) {
     for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
       for (int g = 0; g < G; ++g) acc[g] = mfma_16x16x32(ahi[kc], bq[g][kc], acc[g]);
+    // one wave-uniform decision per tile: every group of the wave unmasked
+    if (tile_ok && (!p.causal || 16 * t + 15 <= tok0) && (tok0 + 16 * G <= p.N)) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int gmin = tok0 + 16 * g;
-      const bool fast = tile_ok && (!p.causal || 16 * t + 15 <= gmin) && (gmin + 16 <= p.N);
-      if (fast) {
+      for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
-      } else {
-        const int n = gmin + col;
+    } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) topk_insert(tk[g], masked_key(p, b, h, n, m0 + r, acc[g][r]));
+      for (int g = 0; g < G; ++g) {
+        const int gmin = tok0 + 16 * g;
+        const bool fast = tile_ok && (!p.causal || 16 * t + 15 <= gmin) && (gmin + 16 <= p.N);
+        if (fast) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
+        } else {
+          const int n = gmin + col;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) topk_insert(tk[g], masked_key(p, b, h, n, m0 + r, acc[g][r]));
+        }
       }
     }
   }
@@ -352,17 +362,25 @@ __global__ __launch_bounds__(256) void sa_kernel32(SAParams p) {
     }
     const int m0 = 16 * t + 4 * quad;
     const bool tile_ok = plain && (16 * t + 16 <= p.em);
+    // one wave-uniform decision per tile: every group of the wave unmasked
+    if (tile_ok && (!p.causal || 16 * t + 15 <= tok0) && (tok0 + 16 * G <= p.N)) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int gmin = tok0 + 16 * g;
-      const bool fast = tile_ok && (!p.causal || 16 * t + 15 <= gmin) && (gmin + 16 <= p.N);
-      if (fast) {
+      for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
-      } else {
-        const int n = gmin + col;
+    } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) topk_insert(tk[g], masked_key(p, b, h, n, m0 + r, acc[g][r]));
+      for (int g = 0; g < G; ++g) {
+        const int gmin = tok0 + 16 * g;
+        const bool fast = tile_ok && (!p.causal || 16 * t + 15 <= gmin) && (gmin + 16 <= p.N);
+        if (fast) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
+        } else {
+          const int n = gmin + col;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) topk_insert(tk[g], masked_key(p, b, h, n, m0 + r, acc[g][r]));
+        }
       }
     }
   }
@@ -502,15 +520,17 @@ __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p,
 template <typename T, int DP>
 hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
   const int Mp = (p.M + 15) & ~15;
-  dim3 grid((p.N + SAShape<DP>::TOK - 1) / SAShape<DP>::TOK, p.B * p.H);
   if constexpr (sizeof(T) == 2) {
+    using S = SAShape<DP, SA16_WAVES>;
+    dim3 grid((p.N + S::TOK - 1) / S::TOK, p.B * p.H);
     const size_t lds = 2 * (size_t)Mp * (DP + 8) * sizeof(T);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sa_kernel16<T, DP>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((sa_kernel16<T, DP>), grid, dim3(256), lds, st, p);
+    hipLaunchKernelGGL((sa_kernel16<T, DP>), grid, dim3(64 * SA16_WAVES), lds, st, p);
   } else {
+    dim3 grid((p.N + SAShape<DP>::TOK - 1) / SAShape<DP>::TOK, p.B * p.H);
     const size_t lds = (size_t)Mp * (DP + 4) * sizeof(float);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sa_kernel32<DP>),
