@@ -197,9 +197,19 @@ struct RoundPtrs {
 // Token-side kernels that gather slot rows stage the float32 [M, D] table of
 // the (b,h) in LDS (row stride DP + 4 floats, zero past D), eight float4
 // loads in flight per thread.  Rows past M are not written.
+// Row stride (floats) of a slot table staged in LDS: unpadded 256-byte rows
+// at d = 64 (the split lane layout keeps its reads conflict-free there), one
+// 16-byte pad otherwise.
+template <int DP>
+constexpr int table_stride() { return DP == 64 ? 64 : DP + 4; }
+// Split-layout half order of this thread's token (see split_dim): odd tokens
+// swap at d = 64.
+template <int DP>
+__device__ __forceinline__ int tok_swap() { return DP == 64 ? (int)((threadIdx.x >> 3) & 1) : 0; }
+
 template <int DP>
 __device__ __forceinline__ void stage_table(float* __restrict__ dst, const float* __restrict__ src, int M, int D) {
-  constexpr int RSD = DP + 4;
+  constexpr int RSD = table_stride<DP>();
   constexpr int STB = 8;
   const int nq = M * (DP / 4);
   const bool vec4 = (D & 3) == 0;
@@ -263,6 +273,82 @@ __device__ __forceinline__ void unraw8(const Raw8<T>& r, float (&o)[8], bool liv
   const T* e = reinterpret_cast<const T*>(&r);
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = live ? to_f(e[i]) : 0.f;
+}
+
+// Split lane layout of the staged-table kernels: lane dc of a token owns the
+// 4-dim groups at 4dc and DP/2 + 4dc, so the token's lanes read one
+// contiguous half of a table row per 16-byte LDS read.  With `sw` set the
+// token takes the halves in the other order; at d = 64 (unpadded 256-byte
+// rows) odd tokens set it, so the two tokens of a 16-lane read cover the two
+// halves of the 64 banks and never meet.  Element i < 4 of the 8 is dim
+// first + i, element i >= 4 is dim second + i - 4.
+template <int DP>
+__device__ __forceinline__ int split_dim(int dc, int sw, int i) {
+  const int lo = 4 * dc, hi = DP / 2 + 4 * dc;
+  return i < 4 ? (sw ? hi : lo) + i : (sw ? lo : hi) + (i - 4);
+}
+template <int DP>
+__device__ __forceinline__ void lds8s(const float* __restrict__ row, int dc, int sw, float (&o)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(row + split_dim<DP>(dc, sw, 0));
+  const float4 b = *reinterpret_cast<const float4*>(row + split_dim<DP>(dc, sw, 4));
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+// WIDE: rows 16-byte aligned and D % 4 == 0: two unconditional loads of 4
+// elements (groups past D re-read dim 0; unraw8s zeroes them).
+template <typename T, bool WIDE, int DP>
+__device__ __forceinline__ Raw8<T> raw8s(const T* __restrict__ row, int dc, int sw, int D) {
+  Raw8<T> r;
+  const int da = split_dim<DP>(dc, sw, 0), db = split_dim<DP>(dc, sw, 4);
+  if constexpr (WIDE) {
+    const int ea = da < D ? da : 0, eb = db < D ? db : 0;
+    if constexpr (sizeof(T) == 2) {
+      const uint2 x = *reinterpret_cast<const uint2*>(row + ea);
+      const uint2 y = *reinterpret_cast<const uint2*>(row + eb);
+      r.u[0] = make_uint4(x.x, x.y, y.x, y.y);
+    } else {
+      r.u[0] = *reinterpret_cast<const uint4*>(row + ea);
+      r.u[1] = *reinterpret_cast<const uint4*>(row + eb);
+    }
+  } else {
+    T* e = reinterpret_cast<T*>(&r);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int d = split_dim<DP>(dc, sw, i);
+      e[i] = d < D ? row[d] : from_f<T>(0.f);
+    }
+  }
+  return r;
+}
+template <typename T, int DP>
+__device__ __forceinline__ void unraw8s(const Raw8<T>& r, float (&o)[8], int dc, int sw, int D, bool live = true) {
+  const T* e = reinterpret_cast<const T*>(&r);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = (live && split_dim<DP>(dc, sw, i) < D) ? to_f(e[i]) : 0.f;
+}
+template <typename T, int DP>
+__device__ __forceinline__ void store8s(T* __restrict__ row, int dc, int sw, int D, bool vec, const float (&v)[8]) {
+  if (vec && (D & 3) == 0) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int d = split_dim<DP>(dc, sw, 4 * g);
+      if (d >= D) continue;
+      if constexpr (sizeof(T) == 2) {
+        T e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = from_f<T>(v[4 * g + i]);
+        *reinterpret_cast<uint2*>(row + d) = *reinterpret_cast<const uint2*>(e);
+      } else {
+        *reinterpret_cast<float4*>(row + d) = make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int d = split_dim<DP>(dc, sw, i);
+      if (d < D) row[d] = from_f<T>(v[i]);
+    }
+  }
 }
 
 // 8 floats of a staged table row (16-byte aligned: d0 % 8 == 0)

@@ -449,31 +449,31 @@ __global__ __launch_bounds__(256) void gather_out_kernel(OutParams p) {
 }
 
 // Staged variant: one block per (b,h) and token chunk; each round's value
-// table is staged in LDS (row stride DP + 4) in turn and every thread keeps
+// table is staged in LDS (row stride table_stride) in turn and every thread keeps
 // the outputs of its GO_PASSES tokens in registers across the rounds.
 constexpr int GO_THREADS = 512;
 constexpr int GO_PASSES = 8;
 
 template <typename T, int DP, bool WIDE>
 __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p, int nchunk) {
-  constexpr int DCH = DP / 8, TPP = GO_THREADS / DCH, RSD = DP + 4;
+  constexpr int DCH = DP / 8, TPP = GO_THREADS / DCH, RSD = table_stride<DP>();
   extern __shared__ __align__(16) unsigned char smem[];
   float* tab = reinterpret_cast<float*>(smem);
   int bh, chunk;
   if (!tok_block(p.B * p.H, nchunk, bh, chunk)) return;
   const int b = bh / p.H, h = bh % p.H;
-  const int dc = threadIdx.x % DCH, d0 = dc * 8;
+  const int dc = threadIdx.x % DCH, sw = tok_swap<DP>();
   const int c_beg = chunk * GO_PASSES * TPP;
   float acc[GO_PASSES][8];
   if (p.base.p) {  // every pass's residual row in flight before any is converted
     Raw8<T> rb[GO_PASSES];
 #pragma unroll
     for (int q = 0; q < GO_PASSES; ++q)
-      rb[q] = raw8<T, WIDE>(tok_row<T>(p.base, b, h, min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1)), d0,
-                            p.D);
+      rb[q] = raw8s<T, WIDE, DP>(tok_row<T>(p.base, b, h, min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1)),
+                                 dc, sw, p.D);
 #pragma unroll
     for (int q = 0; q < GO_PASSES; ++q)
-      unraw8<T>(rb[q], acc[q], d0 < p.D && c_beg + q * TPP + (int)threadIdx.x / DCH < p.N);
+      unraw8s<T, DP>(rb[q], acc[q], dc, sw, p.D, c_beg + q * TPP + (int)threadIdx.x / DCH < p.N);
   } else {
 #pragma unroll
     for (int q = 0; q < GO_PASSES; ++q)
@@ -504,7 +504,7 @@ __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p,
 #pragma unroll
       for (int j = 0; j < KN; ++j) {
         float v[8];
-        lds8(tab + sl[j] * RSD, d0, v);
+        lds8s<DP>(tab + sl[j] * RSD, dc, sw, v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[q][i] += wv[q][j] * v[i];
       }
@@ -513,7 +513,7 @@ __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p,
 #pragma unroll
   for (int q = 0; q < GO_PASSES; ++q) {
     const int n = c_beg + q * TPP + threadIdx.x / DCH;
-    if (n < p.N) store8<T>(tok_row_mut<T>(p.out, b, h, n), d0, p.D, p.out.vec, acc[q]);
+    if (n < p.N) store8s<T, DP>(tok_row_mut<T>(p.out, b, h, n), dc, sw, p.D, p.out.vec, acc[q]);
   }
 }
 
@@ -543,12 +543,12 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
 
 template <typename T, int DP>
 hipError_t launch_out_t(const OutParams& p, hipStream_t st) {
-  const size_t lds = (size_t)p.M * (DP + 4) * 4;
+  const size_t lds = (size_t)p.M * table_stride<DP>() * 4;
   if (lds <= 150 * 1024) {
     constexpr int TPP = GO_THREADS / (DP / 8);
     const int BH = p.B * p.H;
     const int nchunk = (p.N + GO_PASSES * TPP - 1) / (GO_PASSES * TPP);
-    const bool wide = (!p.base.p || p.base.vec) && p.D % 8 == 0;
+    const bool wide = (!p.base.p || p.base.vec) && p.D % 4 == 0;
     const void* fn = wide ? reinterpret_cast<const void*>(&gather_out_lds_kernel<T, DP, true>)
                           : reinterpret_cast<const void*>(&gather_out_lds_kernel<T, DP, false>);
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void tok_grad_kernel(TokGradParams p) {
 
 // ---------------------------------------------------------------------------
 // Staged variants: one block per (b,h) and token chunk stages the round's
-// float32 slot tables in LDS (row stride DP + 4), so the per-token gathers of
+// float32 slot tables in LDS (row stride table_stride), so the per-token gathers of
 // seven slot rows are LDS reads instead of L2 traffic.  Used when the tables
 // fit (e.g. M = 256, d = 64: 64 KiB per table).
 // ---------------------------------------------------------------------------
@@ -168,7 +168,7 @@ template <int DP>
 struct TokShape {
   static constexpr int DCH = DP / 8;                   // lanes per token
   static constexpr int TPP = TOKS_THREADS / DCH;       // tokens per pass
-  static constexpr int RSD = DP + 4;                   // staged row stride
+  static constexpr int RSD = table_stride<DP>();       // staged row stride
 };
 
 template <typename T, int DP, int NP, bool HV, bool WIDE>
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
   if (!tok_block(p.B * p.H, nchunk, bh, chunk)) return;
   const int b = bh / p.H, h = bh % p.H;
   const bool has_g = p.sv != nullptr, has_k = p.dkk != nullptr;
-  const int dc = threadIdx.x % DCH, d0 = dc * 8;
+  const int dc = threadIdx.x % DCH, sw = tok_swap<DP>();
   const int c_beg = chunk * NP * TPP;
   // every global load of the block is issued first: index rows, token rows
   // and (lane dc < 7) weight j = dc of each of the NP passes, then the tables
@@ -198,9 +198,9 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
     const int n = min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1);
     const int64_t row = (int64_t)bh * p.N + n;
     ix[q] = *reinterpret_cast<const uint4*>(p.idx + row * IDX_ROW);
-    rg[q] = raw8<T, WIDE>(tok_row<T>(vg, b, h, n), d0, p.D);
-    rk[q] = raw8<T, WIDE>(tok_row<T>(vk, b, h, n), d0, p.D);
-    if constexpr (HV) rv[q] = raw8<T, WIDE>(tok_row<T>(p.tv, b, h, n), d0, p.D);
+    rg[q] = raw8s<T, WIDE, DP>(tok_row<T>(vg, b, h, n), dc, sw, p.D);
+    rk[q] = raw8s<T, WIDE, DP>(tok_row<T>(vk, b, h, n), dc, sw, p.D);
+    if constexpr (HV) rv[q] = raw8s<T, WIDE, DP>(tok_row<T>(p.tv, b, h, n), dc, sw, p.D);
 #pragma unroll
     for (int u = 0; u < JPL; ++u) {
       const int j = dc + u * DCH;
@@ -226,25 +226,25 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
     const uint32_t sl[KN] = {ir.x & 0xFFFF, ir.x >> 16, ir.y & 0xFFFF, ir.y >> 16,
                              ir.z & 0xFFFF, ir.z >> 16, ir.w & 0xFFFF};
     float g[8], a[8], c[8];
-    if (has_g) unraw8<T>(rg[q], g, d0 < p.D);
-    if (has_k) unraw8<T>(rk[q], a, d0 < p.D);
-    if constexpr (HV) unraw8<T>(rv[q], c, d0 < p.D);
+    if (has_g) unraw8s<T, DP>(rg[q], g, dc, sw, p.D);
+    if (has_k) unraw8s<T, DP>(rk[q], a, dc, sw, p.D);
+    if constexpr (HV) unraw8s<T, DP>(rv[q], c, dc, sw, p.D);
     float dw[KN];
 #pragma unroll
     for (int j = 0; j < KN; ++j) {
       float sacc = 0.f, v[8];
       if (has_g) {
-        lds8(tsv + sl[j] * RSD, d0, v);
+        lds8s<DP>(tsv + sl[j] * RSD, dc, sw, v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) sacc += g[i] * v[i];
       }
       if (has_k) {
-        lds8(tdk + sl[j] * RSD, d0, v);
+        lds8s<DP>(tdk + sl[j] * RSD, dc, sw, v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) sacc += a[i] * v[i];
       }
       if constexpr (HV) {
-        lds8(tdv + sl[j] * RSD, d0, v);
+        lds8s<DP>(tdv + sl[j] * RSD, dc, sw, v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) sacc += c[i] * v[i];
       }
@@ -292,7 +292,7 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParam
   const int b = bh / p.H, h = bh % p.H;
   float* t0 = reinterpret_cast<float*>(smem);
   const int64_t tb = (int64_t)bh * p.M * p.D;
-  const int dc = threadIdx.x % DCH, d0 = dc * 8;
+  const int dc = threadIdx.x % DCH, sw = tok_swap<DP>();
   const int c_beg = chunk * PASSES * TPP;
   constexpr int PK = KV ? PASSES : 1;  // token-key / token-value gradients (legacy form only)
   float aq[PASSES][8], ak[PK][8], av[PK][8];
@@ -300,10 +300,10 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParam
     Raw8<T> rg[PASSES];
 #pragma unroll
     for (int q = 0; q < PASSES; ++q)
-      rg[q] = raw8<T, WIDE>(tok_row<T>(p.g, b, h, min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1)), d0, p.D);
+      rg[q] = raw8s<T, WIDE, DP>(tok_row<T>(p.g, b, h, min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1)), dc, sw, p.D);
 #pragma unroll
     for (int q = 0; q < PASSES; ++q)
-      unraw8<T>(rg[q], aq[q], d0 < p.D && c_beg + q * TPP + (int)threadIdx.x / DCH < p.N);
+      unraw8s<T, DP>(rg[q], aq[q], dc, sw, p.D, c_beg + q * TPP + (int)threadIdx.x / DCH < p.N);
   } else {
 #pragma unroll
     for (int q = 0; q < PASSES; ++q)
@@ -353,13 +353,13 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParam
         float v[8];
         if (use_sk) {
           const float cj = p.c * dsr[j];
-          lds8(tsk + sl[j] * RSD, d0, v);
+          lds8s<DP>(tsk + sl[j] * RSD, dc, sw, v);
 #pragma unroll
           for (int i = 0; i < 8; ++i) aq[q][i] += cj * v[i];
         }
         const float wj = wr[j];
         if (p.dkk[r]) {
-          lds8(tdk + sl[j] * RSD, d0, v);
+          lds8s<DP>(tdk + sl[j] * RSD, dc, sw, v);
           if constexpr (KV) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) ak[q][i] += wj * v[i];
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParam
         }
         if constexpr (KV) {
           if (p.dkv[r]) {
-            lds8(tdv + sl[j] * RSD, d0, v);
+            lds8s<DP>(tdv + sl[j] * RSD, dc, sw, v);
 #pragma unroll
             for (int i = 0; i < 8; ++i) av[q][i] += wj * v[i];
           }
@@ -382,10 +382,10 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParam
   for (int q = 0; q < PASSES; ++q) {
     const int n = c_beg + q * TPP + threadIdx.x / DCH;
     if (n >= p.N) continue;
-    if (p.dq.p) store8<T>(tok_row_mut<T>(p.dq, b, h, n), d0, p.D, p.dq.vec, aq[q]);
+    if (p.dq.p) store8s<T, DP>(tok_row_mut<T>(p.dq, b, h, n), dc, sw, p.D, p.dq.vec, aq[q]);
     if constexpr (KV) {
-      if (p.dtk.p) store8<T>(tok_row_mut<T>(p.dtk, b, h, n), d0, p.D, p.dtk.vec, ak[q]);
-      if (p.dtv.p) store8<T>(tok_row_mut<T>(p.dtv, b, h, n), d0, p.D, p.dtv.vec, av[q]);
+      if (p.dtk.p) store8s<T, DP>(tok_row_mut<T>(p.dtk, b, h, n), dc, sw, p.D, p.dtk.vec, ak[q]);
+      if (p.dtv.p) store8s<T, DP>(tok_row_mut<T>(p.dtv, b, h, n), dc, sw, p.D, p.dtv.vec, av[q]);
     }
   }
 }
@@ -442,12 +442,13 @@ hipError_t launch_attend_idx_t(const AttendIdxParams& p, hipStream_t st) {
 
 // staged tables fit one block's LDS (leave room for a second block's worth of nothing)
 inline bool tables_fit(int nt, int M, int DP) {
-  return (size_t)nt * M * (DP + 4) * 4 + (size_t)M * 4 <= 150 * 1024;
+  const int rsd = DP == 64 ? 64 : DP + 4;  // table_stride<DP>()
+  return (size_t)nt * M * rsd * 4 + (size_t)M * 4 <= 150 * 1024;
 }
 
-// 16-byte token loads for every row the kernel reads (see raw8)
+// unconditional token loads for every row the kernel reads (see raw8s)
 inline bool wide_rows(std::initializer_list<const TokView*> views, int D) {
-  if (D % 8 != 0) return false;
+  if (D % 4 != 0) return false;
   for (const TokView* v : views)
     if (v->p && !v->vec) return false;
   return true;
