@@ -135,14 +135,19 @@ __device__ __forceinline__ float key_score(float k, uint32_t hi_mask) {
 constexpr float MASKED_SCORE = -3.4028234663852886e38f;  // -FLT_MAX
 __device__ __forceinline__ bool key_masked(float k) { return k <= -1.0e38f; }
 
+// Insert x into the descending list a (keeps the K largest): one med3 per
+// entry and one max for the head, as a plain v_max_f32 (fmaxf would add
+// NaN-quieting maxes on both operands; keys here are finite or -inf).
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 template <int K>
 __device__ __forceinline__ void topk_insert(float (&a)[K], float x) {
-  float b[K];
-  b[0] = fmaxf(a[0], x);
 #pragma unroll
-  for (int j = 1; j < K; ++j) b[j] = __builtin_amdgcn_fmed3f(a[j - 1], a[j], x);
-#pragma unroll
-  for (int j = 0; j < K; ++j) a[j] = b[j];
+  for (int j = K - 1; j >= 1; --j) a[j] = __builtin_amdgcn_fmed3f(a[j - 1], a[j], x);
+  a[0] = max_raw(a[0], x);
 }
 
 // ------------------------------------------------------------------ MFMA ---

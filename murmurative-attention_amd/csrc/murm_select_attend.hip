@@ -214,10 +214,13 @@ __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
       for (int g = 0; g < G; ++g) acc[g] = mfma_16x16x32(ahi[kc], bq[g][kc], acc[g]);
     // one wave-uniform decision per tile: every group of the wave unmasked
     if (tile_ok && (!p.causal || 16 * t + 15 <= tok0) && (tok0 + 16 * G <= p.N)) {
+      uint32_t mr[4];  // slot ids of this lane's four rows, shared by the groups
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mr[r] = (uint32_t)(m0 + r);
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
+        for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, mr[r]));
     } else {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -364,10 +367,13 @@ __global__ __launch_bounds__(256) void sa_kernel32(SAParams p) {
     const bool tile_ok = plain && (16 * t + 16 <= p.em);
     // one wave-uniform decision per tile: every group of the wave unmasked
     if (tile_ok && (!p.causal || 16 * t + 15 <= tok0) && (tok0 + 16 * G <= p.N)) {
+      uint32_t mr[4];  // slot ids of this lane's four rows, shared by the groups
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mr[r] = (uint32_t)(m0 + r);
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
+        for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, mr[r]));
     } else {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
