@@ -802,21 +802,16 @@ int murm_murmurate_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
       s.combine_dk = shared;
       s.dk_out = G.dk[r - 1]; s.dv_out = G.dv[r - 1]; s.dW_out = G.dW[r - 1];
       s.carry_k_out = G.ck[r & 1]; s.carry_v_out = G.cv[r & 1];
-    } else {
+    } else {  // the first round's slot grads go straight to the caller's tensors
       s.final_out = 1;
       s.gk_out = G.Gk; s.gv_out = G.Gv;
+      s.gk_t = grad_sk; s.gv_t = grad_sv;
+      s.gt_sb = (int64_t)H * M * D; s.gt_sh = (int64_t)M * D; s.gt_sm = D;
+      s.gt_dtype = slot_dtype;
     }
     RUN(C_SEGB, "seg_attbwd", launch_seg(dtype, DP, SEG_ATTBWD, s, &G.part, 0, st));
     if (seg_two_stage(dtype, DP, SEG_ATTBWD, s, &G.part))
       RUN(C_SEGBR, "seg_attbwd_reduce", launch_seg(dtype, DP, SEG_ATTBWD, s, &G.part, 1, st));
-    if (r == 0) {
-      const int64_t ssb = (int64_t)H * M * D, ssh = (int64_t)M * D, ssm = D;
-      {
-        const SlotConv<const float*, void*> ca{G.Gk, ssb, ssh, ssm, grad_sk};
-        const SlotConv<const float*, void*> cb{G.Gv, ssb, ssh, ssm, grad_sv};
-        RUN(C_CONV, "from_state", launch_from_state2(slot_dtype, ca, &cb, B, H, M, D, st));
-      }
-    }
   }
 
   TokGradParams tg{};

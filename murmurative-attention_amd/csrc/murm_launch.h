@@ -53,6 +53,9 @@ struct SegParams {
   const float* carry_k; const float* carry_v;  // optional pass-through grads (read, halo included)
   int final_out;                               // 1: write G'' of the owned rows to gk_out / gv_out
   float* gk_out; float* gv_out;                // fp32 [BH, M, D]
+  void* gk_t; void* gv_t;                      // or (non-null) the slot-dtype [B,H,M,D] grads directly
+  int64_t gt_sb, gt_sh, gt_sm;                 //   their element strides
+  int gt_dtype;                                //   and dtype code
   // ATTBWD epilogue for the previous round (final_out == 0)
   const float* Kp; const float* Vp; const float* Wp;  // that round's forward sums
   int combine_dk;                              // token keys == token values: dk_out = dKk + dKv

@@ -114,12 +114,28 @@ __device__ void attbwd_epilogue(const SegParams& p, int bh, int g0, int halo, in
   }
   __syncthreads();
   if (p.final_out) {
+    const int b = bh / p.H, h = bh % p.H;
     for (int i = threadIdx.x; i < GS * DP; i += blockDim.x) {
       const int own = i / DP, d = i % DP, m = g0 + own;
       if (m >= p.M || d >= p.D) continue;
-      const int64_t o = base + (int64_t)m * p.D + d;
-      p.gk_out[o] = accA[(own + halo) * DP + d];
-      p.gv_out[o] = accB[(own + halo) * DP + d];
+      const float gk = accA[(own + halo) * DP + d], gv = accB[(own + halo) * DP + d];
+      if (p.gk_t) {  // the caller's slot-gradient tensors, converted here
+        const int64_t t = b * p.gt_sb + h * p.gt_sh + (int64_t)m * p.gt_sm + d;
+        if (p.gt_dtype == DT_BF16) {
+          static_cast<__bf16*>(p.gk_t)[t] = (__bf16)gk;
+          static_cast<__bf16*>(p.gv_t)[t] = (__bf16)gv;
+        } else if (p.gt_dtype == DT_F16) {
+          static_cast<_Float16*>(p.gk_t)[t] = (_Float16)gk;
+          static_cast<_Float16*>(p.gv_t)[t] = (_Float16)gv;
+        } else {
+          static_cast<float*>(p.gk_t)[t] = gk;
+          static_cast<float*>(p.gv_t)[t] = gv;
+        }
+      } else {
+        const int64_t o = base + (int64_t)m * p.D + d;
+        p.gk_out[o] = gk;
+        p.gv_out[o] = gv;
+      }
     }
     return;
   }
