@@ -143,11 +143,57 @@ __device__ __forceinline__ float max_raw(float a, float b) {
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
+__device__ __forceinline__ float min_raw(float a, float b) {
+  float r;
+  asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 template <int K>
 __device__ __forceinline__ void topk_insert(float (&a)[K], float x) {
 #pragma unroll
   for (int j = K - 1; j >= 1; --j) a[j] = __builtin_amdgcn_fmed3f(a[j - 1], a[j], x);
   a[0] = max_raw(a[0], x);
+}
+
+// The 7 largest of two descending lists of 7, descending.  c_j =
+// max(a_j, b_{6-j}) holds them as a V-shaped (bitonic) sequence; with +inf
+// appended it stays bitonic, and the 8-wide bitonic merge network (distance
+// 4, 2, 1) sorts it.  The +inf entry only moves one element per stage, so
+// 7 max + 9 compare-exchanges = 25 VALU (7 insertions would take 49).
+__device__ __forceinline__ void ce_raw(float& hi, float& lo) {
+  const float h = max_raw(hi, lo), l = min_raw(hi, lo);
+  hi = h;
+  lo = l;
+}
+__device__ __forceinline__ void top7_merge(const float (&a)[7], const float (&b)[7], float (&out)[7]) {
+  float c[8];
+#pragma unroll
+  for (int j = 0; j < 7; ++j) c[j] = max_raw(a[j], b[6 - j]);
+  ce_raw(c[0], c[4]); ce_raw(c[1], c[5]); ce_raw(c[2], c[6]); c[7] = c[3];  // c[3] <- +inf
+  ce_raw(c[0], c[2]); c[3] = c[1]; ce_raw(c[4], c[6]); ce_raw(c[5], c[7]);  // c[1] <- +inf
+  ce_raw(c[2], c[3]); ce_raw(c[4], c[5]); ce_raw(c[6], c[7]);               // c[0] -> second
+  out[0] = c[0]; out[1] = c[2]; out[2] = c[3]; out[3] = c[4];
+  out[4] = c[5]; out[5] = c[6]; out[6] = c[7];
+}
+
+// Values of lanes l and l ^ X (X = 16 or 32) without an LDS round trip:
+// v_permlane{16,32}_swap_b32 on two copies of v exchange the odd rows (X = 16)
+// or the upper half (X = 32) of the first copy with the even rows / lower half
+// of the second, so both lanes of a pair end up holding (value of the lower
+// lane, value of the upper lane) in the same order.
+template <int X>
+__device__ __forceinline__ void lane_pair(float v, float& lower, float& upper) {
+  const uint32_t u = __float_as_uint(v);
+  if constexpr (X == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    lower = __uint_as_float(r[0]);
+    upper = __uint_as_float(r[1]);
+  } else {
+    static_assert(X == 32, "lane_pair: X is 16 or 32");
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    lower = __uint_as_float(r[0]);
+    upper = __uint_as_float(r[1]);
+  }
 }
 
 // ------------------------------------------------------------------ MFMA ---

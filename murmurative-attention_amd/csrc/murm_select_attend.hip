@@ -50,14 +50,13 @@ template <int G>
 __device__ __forceinline__ void merge_quads(float (&tk)[G][KN]) {
 #pragma unroll
   for (int g = 0; g < G; ++g) {
+    float lo[KN], up[KN];
 #pragma unroll
-    for (int x = 16; x <= 32; x <<= 1) {
-      float o[KN];
+    for (int j = 0; j < KN; ++j) lane_pair<16>(tk[g][j], lo[j], up[j]);
+    top7_merge(lo, up, tk[g]);
 #pragma unroll
-      for (int j = 0; j < KN; ++j) o[j] = shfl_xor_f(tk[g][j], x);
-#pragma unroll
-      for (int j = 0; j < KN; ++j) topk_insert(tk[g], o[j]);
-    }
+    for (int j = 0; j < KN; ++j) lane_pair<32>(tk[g][j], lo[j], up[j]);
+    top7_merge(lo, up, tk[g]);
   }
 }
 
@@ -166,7 +165,8 @@ __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
   }
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int quad = lane >> 4, col = lane & 15;
   const int tok0 = blockIdx.x * SAShape<DP, SA16_WAVES>::TOK + wave * (G * 16);
   if (tok0 >= p.N) return;  // whole wave past the end (no block-wide sync below)
@@ -189,9 +189,8 @@ __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
 #pragma unroll
     for (int j = 0; j < KN; ++j) tk[g][j] = -INFINITY;
 
-  const bool plain = !p.mask && !p.bias;
-  const int nT = Mp / 16;
-  for (int t = 0; t < nT; ++t) {
+  // scores of slot tile t (16 slots) against the wave's G token groups
+  auto scores = [&](int t, f32x4 (&acc)[G]) {
     V ahi[KC], alo[KC];
     const int arow = 16 * t + col;
 #pragma unroll
@@ -199,9 +198,6 @@ __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
       ahi[kc] = *reinterpret_cast<const V*>(lhi + arow * ROW + 32 * kc + 8 * quad);
       alo[kc] = *reinterpret_cast<const V*>(llo + arow * ROW + 32 * kc + 8 * quad);
     }
-    const int m0 = 16 * t + 4 * quad;
-    const bool tile_ok = plain && (16 * t + 16 <= p.em);
-    f32x4 acc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -212,28 +208,45 @@ __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
     for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
       for (int g = 0; g < G; ++g) acc[g] = mfma_16x16x32(ahi[kc], bq[g][kc], acc[g]);
-    // one wave-uniform decision per tile: every group of the wave unmasked
-    if (tile_ok && (!p.causal || 16 * t + 15 <= tok0) && (tok0 + 16 * G <= p.N)) {
-      uint32_t mr[4];  // slot ids of this lane's four rows, shared by the groups
+  };
+
+  // Tiles [0, nfast) mask no score of the wave (every token in range, slots
+  // below effective_M, inside the causal prefix): a branch-free loop.  The
+  // rest take the per-group test and, where needed, the masked path.
+  const bool plain = !p.mask && !p.bias;
+  const int nT = Mp / 16;
+  int nfast = 0;
+  if (plain && tok0 + 16 * G <= p.N) {
+    nfast = min(nT, p.em / 16);
+    if (p.causal) nfast = min(nfast, (tok0 + 1) / 16);
+  }
+  for (int t = 0; t < nfast; ++t) {
+    f32x4 acc[G];
+    scores(t, acc);
+    uint32_t mr[4];  // slot ids of this lane's four rows, shared by the groups
 #pragma unroll
-      for (int r = 0; r < 4; ++r) mr[r] = (uint32_t)(m0 + r);
+    for (int r = 0; r < 4; ++r) mr[r] = (uint32_t)(16 * t + 4 * quad + r);
 #pragma unroll
-      for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, mr[r]));
-    } else {
+      for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, mr[r]));
+  }
+  for (int t = nfast; t < nT; ++t) {
+    f32x4 acc[G];
+    scores(t, acc);
+    const int m0 = 16 * t + 4 * quad;
+    const bool tile_ok = plain && (16 * t + 16 <= p.em);
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const int gmin = tok0 + 16 * g;
-        const bool fast = tile_ok && (!p.causal || 16 * t + 15 <= gmin) && (gmin + 16 <= p.N);
-        if (fast) {
+    for (int g = 0; g < G; ++g) {
+      const int gmin = tok0 + 16 * g;
+      const bool fast = tile_ok && (!p.causal || 16 * t + 15 <= gmin) && (gmin + 16 <= p.N);
+      if (fast) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
-        } else {
-          const int n = gmin + col;
+        for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
+      } else {
+        const int n = gmin + col;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) topk_insert(tk[g], masked_key(p, b, h, n, m0 + r, acc[g][r]));
-        }
+        for (int r = 0; r < 4; ++r) topk_insert(tk[g], masked_key(p, b, h, n, m0 + r, acc[g][r]));
       }
     }
   }
@@ -328,7 +341,8 @@ __global__ __launch_bounds__(256) void sa_kernel32(SAParams p) {
   }
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int quad = lane >> 4, col = lane & 15;
   const int tok0 = blockIdx.x * SAShape<DP>::TOK + wave * (G * 16);
   if (tok0 >= p.N) return;
@@ -350,11 +364,8 @@ __global__ __launch_bounds__(256) void sa_kernel32(SAParams p) {
 #pragma unroll
     for (int j = 0; j < KN; ++j) tk[g][j] = -INFINITY;
 
-  const bool plain = !p.mask && !p.bias;
-  const int nT = Mp / 16;
-  for (int t = 0; t < nT; ++t) {
+  auto scores = [&](int t, f32x4 (&acc)[G]) {
     const float* arow = lsk + (16 * t + col) * ROW + quad;
-    f32x4 acc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -363,30 +374,43 @@ __global__ __launch_bounds__(256) void sa_kernel32(SAParams p) {
 #pragma unroll
       for (int g = 0; g < G; ++g) acc[g] = mfma_16x16x4(a, bq[g][kk], acc[g]);
     }
+  };
+
+  // tiles [0, nfast): no masked score in the wave (as in sa_kernel16)
+  const bool plain = !p.mask && !p.bias;
+  const int nT = Mp / 16;
+  int nfast = 0;
+  if (plain && tok0 + 16 * G <= p.N) {
+    nfast = min(nT, p.em / 16);
+    if (p.causal) nfast = min(nfast, (tok0 + 1) / 16);
+  }
+  for (int t = 0; t < nfast; ++t) {
+    f32x4 acc[G];
+    scores(t, acc);
+    uint32_t mr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mr[r] = (uint32_t)(16 * t + 4 * quad + r);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, mr[r]));
+  }
+  for (int t = nfast; t < nT; ++t) {
+    f32x4 acc[G];
+    scores(t, acc);
     const int m0 = 16 * t + 4 * quad;
     const bool tile_ok = plain && (16 * t + 16 <= p.em);
-    // one wave-uniform decision per tile: every group of the wave unmasked
-    if (tile_ok && (!p.causal || 16 * t + 15 <= tok0) && (tok0 + 16 * G <= p.N)) {
-      uint32_t mr[4];  // slot ids of this lane's four rows, shared by the groups
 #pragma unroll
-      for (int r = 0; r < 4; ++r) mr[r] = (uint32_t)(m0 + r);
+    for (int g = 0; g < G; ++g) {
+      const int gmin = tok0 + 16 * g;
+      const bool fast = tile_ok && (!p.causal || 16 * t + 15 <= gmin) && (gmin + 16 <= p.N);
+      if (fast) {
 #pragma unroll
-      for (int g = 0; g < G; ++g)
+        for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
+      } else {
+        const int n = gmin + col;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, mr[r]));
-    } else {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const int gmin = tok0 + 16 * g;
-        const bool fast = tile_ok && (!p.causal || 16 * t + 15 <= gmin) && (gmin + 16 <= p.N);
-        if (fast) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) topk_insert(tk[g], make_key(acc[g][r], p.hi_mask, (uint32_t)(m0 + r)));
-        } else {
-          const int n = gmin + col;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) topk_insert(tk[g], masked_key(p, b, h, n, m0 + r, acc[g][r]));
-        }
+        for (int r = 0; r < 4; ++r) topk_insert(tk[g], masked_key(p, b, h, n, m0 + r, acc[g][r]));
       }
     }
   }
