@@ -258,9 +258,33 @@ constexpr int table_stride() { return DP == 64 ? 64 : DP + 4; }
 template <int DP>
 __device__ __forceinline__ int tok_swap() { return DP == 64 ? (int)((threadIdx.x >> 3) & 1) : 0; }
 
+// Global -> LDS copy of `bytes` contiguous bytes (a multiple of 16; both
+// ends 16-byte aligned) without a trip through registers: each wave issues
+// global_load_lds_dwordx4 for its 1 KiB pieces (lane l's 16 bytes land at the
+// piece's LDS base + 16 l), all pieces in flight at once, then waits for
+// them.  The caller's barrier publishes the copy to the other waves.
+__device__ __forceinline__ void copy_to_lds(void* dst, const void* src, int bytes) {
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  typedef __attribute__((address_space(1))) void* glb_ptr;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int nw = (int)(blockDim.x >> 6);
+  for (int off = wave * 1024; off < bytes; off += nw * 1024) {
+    const int o = off + lane * 16;
+    if (o < bytes)
+      __builtin_amdgcn_global_load_lds((glb_ptr)((const char*)src + o), (lds_ptr)((char*)dst + off), 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's pieces are in LDS
+}
+
 template <int DP>
 __device__ __forceinline__ void stage_table(float* __restrict__ dst, const float* __restrict__ src, int M, int D) {
   constexpr int RSD = table_stride<DP>();
+  // unpadded rows of the full width: the LDS table is the global one
+  if (RSD == D && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    copy_to_lds(dst, src, M * D * 4);
+    return;
+  }
   constexpr int STB = 8;
   const int nq = M * (DP / 4);
   const bool vec4 = (D & 3) == 0;
