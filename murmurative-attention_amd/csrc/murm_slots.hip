@@ -737,8 +737,30 @@ __global__ __launch_bounds__(RED_THREADS) void seg_reduce_kernel(SegParams p, Pa
   const int64_t cstride = (int64_t)p.B * p.H * p.M * p.D;
   const int nc = pp.nchunk;
   constexpr int QPR = DP / 4;
-  // quads of 4 dims: all chunk loads of a quad are issued before the adds
-  for (int i = threadIdx.x; i < nv * NS * QPR; i += blockDim.x) {
+  // Items: quads of 4 dims of a vector row, then (UPDATE) the weight sum of
+  // each row.  Every item issues its chunk loads in batches of NCB before
+  // adding them in chunk order.
+  const int nquad = nv * NS * QPR;
+  const int nitem = nquad + (MODE == SEG_UPDATE ? NS : 0);
+  for (int i = threadIdx.x; i < nitem; i += blockDim.x) {
+    if (i >= nquad) {
+      const int rel = i - nquad, m = lo + rel;
+      float sw = 0.f;
+      if (m >= 0 && m < p.M) {
+        const float* src = pp.partW + (int64_t)bh * p.M + m;
+        const int64_t ws = (int64_t)p.B * p.H * p.M;
+        for (int c0 = 0; c0 < nc; c0 += NCB) {
+          float x[NCB];
+#pragma unroll
+          for (int c = 0; c < NCB; ++c) x[c] = c0 + c < nc ? src[(c0 + c) * ws] : 0.f;
+#pragma unroll
+          for (int c = 0; c < NCB; ++c)
+            if (c0 + c < nc) sw += x[c];
+        }
+      }
+      accW[rel] = sw;
+      continue;
+    }
     const int v = i / (NS * QPR), rel = (i / QPR) % NS, d = (i % QPR) * 4, m = lo + rel;
     float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
     if (m >= 0 && m < p.M && d < p.D) {
@@ -770,15 +792,6 @@ __global__ __launch_bounds__(RED_THREADS) void seg_reduce_kernel(SegParams p, Pa
     if (sameB) {
       float* accb = accB + rel * DP + d;
       accb[0] = sum.x; accb[1] = sum.y; accb[2] = sum.z; accb[3] = sum.w;
-    }
-  }
-  if (MODE == SEG_UPDATE) {
-    for (int rel = threadIdx.x; rel < NS; rel += blockDim.x) {
-      const int m = lo + rel;
-      float sw = 0.f;
-      if (m >= 0 && m < p.M)
-        for (int c = 0; c < nc; ++c) sw += pp.partW[((int64_t)c * p.B * p.H + bh) * p.M + m];
-      accW[rel] = sw;
     }
   }
   __syncthreads();
