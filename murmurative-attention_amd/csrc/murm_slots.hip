@@ -436,8 +436,11 @@ __global__ __launch_bounds__(1024) void seg_partial_kernel(SegParams p, PartPara
 // per block.  Each vector has its own 4 waves; wave w owns 16-slot tiles
 // w, w+4, ... of the block's slot group and keeps their sums for every dim
 // tile in MFMA accumulators across the chunk; with UPDATE a ones column gives
-// the weight sums.  Fixed
-// k order inside each MFMA and sub-chunks in token order: bitwise
+// the weight sums.  With TG = 2 token groups the block holds two such sets of
+// waves, each with its own LDS staging, over the two halves of the chunk; the
+// upper half's sums are added to the lower half's through LDS at the end, so
+// the block writes one partial for twice the tokens.  Fixed k order inside
+// each MFMA, sub-chunks in token order, halves added lower + upper: bitwise
 // reproducible.
 // ---------------------------------------------------------------------------
 constexpr int MMA_WAVES = 4;       // waves per vector
@@ -453,9 +456,10 @@ __device__ __forceinline__ int swz(int row, int c) {
   return row * ROWB + ((c ^ f) & (CPR - 1)) * 16;
 }
 
-template <int DP, int MODE, int NV, int SUBT>
+template <int DP, int MODE, int NV, int SUBT, int TG = 1>
 struct MmaShape {
-  static constexpr int THREADS = 64 * MMA_WAVES * NV;       // one group of waves per vector
+  static constexpr int GT = 64 * MMA_WAVES * NV;            // threads of a token group: waves per vector
+  static constexpr int THREADS = GT * TG;
   static constexpr int DT = DP / 16;                        // dim tiles
   static constexpr int KINDS = MODE == SEG_ATTBWD ? 2 : 1;  // coefficient kinds (c*ds, w)
   static constexpr int WTILE = MODE == SEG_UPDATE ? 1 : 0;  // ones tile for the weight sums
@@ -464,33 +468,42 @@ struct MmaShape {
   static constexpr int MS_REG = MMA_WAVES * WT * 16;
   static constexpr int MS_LDS = (64 * 1024) / (KINDS * 2 * ROWB);  // C^T within 64 KiB
   static constexpr int MS = MS_REG < MS_LDS ? MS_REG : MS_LDS;    // slots per block
-  static constexpr size_t LDS = (size_t)NV * DP * ROWB + (size_t)KINDS * 2 * MS * ROWB;
+  static constexpr size_t GLDS = (size_t)NV * DP * ROWB + (size_t)KINDS * 2 * MS * ROWB;  // per group
+  static constexpr int NACC = WT * DT + WTILE * WT;         // float4 accumulators per thread
+  static constexpr size_t MERGE = TG > 1 ? (size_t)NACC * GT * 16 : 0;
+  static constexpr size_t LDS = TG * GLDS > MERGE ? TG * GLDS : MERGE;
 };
 
-template <typename T, int DP, int MODE, int NV, int SUBT>
-__global__ __launch_bounds__(64 * MMA_WAVES * NV, 2) void seg_mma_kernel(SegParams p, PartParams pp) {
+template <typename T, int DP, int MODE, int NV, int SUBT, int TG>
+__global__ __launch_bounds__(64 * MMA_WAVES * NV * TG, 2) void seg_mma_kernel(SegParams p, PartParams pp) {
   using V = typename Mfma16<T>::vec;
-  using Sh = MmaShape<DP, MODE, NV, SUBT>;
+  using Sh = MmaShape<DP, MODE, NV, SUBT, TG>;
   constexpr int DT = Sh::DT, KINDS = Sh::KINDS, WT = Sh::WT, MS = Sh::MS, ROWB = Sh::ROWB;
-  constexpr int MMA_THREADS = Sh::THREADS;
+  constexpr int MMA_THREADS = Sh::GT;             // staging and marking run per token group
   constexpr int UPR = DP / 8;                      // 16-byte units per token row
   constexpr int GROUPS = NV * UPR * (SUBT / 4);    // staging items: (vector, unit, 4 tokens)
   constexpr int GPT = (GROUPS + MMA_THREADS - 1) / MMA_THREADS;
   constexpr int TPT = MMA_THREADS / SUBT;          // marking threads per token (one wave)
   constexpr int JPT = (8 + TPT - 1) / TPT;         // js per marking thread
   extern __shared__ __align__(16) unsigned char smem[];
-  unsigned char* xt = smem;                          // [NV*DP rows][ROWB]
-  unsigned char* ct = smem + NV * DP * ROWB;         // [KINDS][hi, lo][MS rows][ROWB]
+  const int tg = TG > 1 ? (int)threadIdx.x / MMA_THREADS : 0;  // token group
+  unsigned char* xt = smem + tg * Sh::GLDS;          // [NV*DP rows][ROWB]
+  unsigned char* ct = xt + NV * DP * ROWB;           // [KINDS][hi, lo][MS rows][ROWB]
 
   int bh, chunk, sg;
   const int nsg = (p.M + MS - 1) / MS;
   part_block(pp.nchunk, nsg, p.B * p.H, bh, chunk, sg);
   if (bh < 0) return;  // whole block, before any barrier
   const int b = bh / p.H, h = bh % p.H;
-  const int c_beg = chunk * pp.chunk_tokens;
-  const int c_end = min(p.N, c_beg + pp.chunk_tokens);
+  // this token group's whole sub-chunks of the chunk (the same count for every group)
+  const int k_beg = chunk * pp.chunk_tokens;
+  const int nsub = (min(p.N, k_beg + pp.chunk_tokens) - k_beg + SUBT - 1) / SUBT;
+  const int per = (nsub + TG - 1) / TG;
+  const int c_beg = k_beg + tg * per * SUBT;
+  const int c_end = min(min(p.N, k_beg + pp.chunk_tokens), c_beg + per * SUBT);
   const int s0 = sg * MS;
-  const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) % MMA_WAVES, vw = (tid >> 6) / MMA_WAVES;
+  const int tid = (int)threadIdx.x % MMA_THREADS, lane = tid & 63, wave = (tid >> 6) % MMA_WAVES,
+            vw = (tid >> 6) / MMA_WAVES;
   const int ms_here = min(MS, p.M - s0);
   const int ntiles = (ms_here + 15) / 16;
 
@@ -668,12 +681,7 @@ __global__ __launch_bounds__(64 * MMA_WAVES * NV, 2) void seg_mma_kernel(SegPara
       a[hl] = *reinterpret_cast<const V*>(ct + (kind * 2 + hl) * MS * ROWB + swz<SUBT>(srow, chk));
   };
 
-  fetch(c_beg);
-  for (int n0 = c_beg; n0 < c_end; n0 += SUBT) {
-    stash(n0);
-    mark(n0);
-    __syncthreads();
-    if (n0 + SUBT < c_end) fetch(n0 + SUBT);  // in flight during the products
+  auto products = [&]() {
 #pragma unroll
     for (int ks = 0; ks < SUBT / 32; ++ks) {
       const int chk = ks * 4 + (lane >> 4);
@@ -699,7 +707,72 @@ __global__ __launch_bounds__(64 * MMA_WAVES * NV, 2) void seg_mma_kernel(SegPara
         a[1] = an[1];
       }
     }
+  };
+
+  fetch(c_beg);
+  if constexpr (TG == 1) {
+    for (int it = 0; it < per; ++it) {
+      const int n0 = c_beg + it * SUBT;
+      stash(n0);
+      mark(n0);
+      __syncthreads();
+      if (it + 1 < per) fetch(n0 + SUBT);  // in flight during the products
+      products();
+      __syncthreads();
+    }
+  } else {
+    // Ping-pong: in each half-step one group stages a sub-chunk while the
+    // other multiplies its previous one, so staging (VALU, LDS stores) and
+    // products (MFMA) overlap across the groups.  A group past its tokens
+    // stages zeros, so both groups run the same barriers.
+    for (int k = 0; k <= per; ++k) {
+      if (tg == 0) {
+        if (k < per) { stash(c_beg + k * SUBT); mark(c_beg + k * SUBT); }
+      } else if (k >= 1) {
+        if (k < per) fetch(c_beg + k * SUBT);
+        products();
+      }
+      __syncthreads();
+      if (k < per) {
+        if (tg == 0) {
+          if (k + 1 < per) fetch(c_beg + (k + 1) * SUBT);
+          products();
+        } else {
+          stash(c_beg + k * SUBT);
+          mark(c_beg + k * SUBT);
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  if constexpr (TG > 1) {  // upper token group's sums added to the lower group's
+    static_assert(TG == 2, "seg_mma_kernel: one or two token groups");
+    float4* mb = reinterpret_cast<float4*>(smem);  // staging is no longer read
+    auto slot4 = [&](int k) -> float4& { return mb[k * MMA_THREADS + tid]; };
+    if (tg == 1) {
+#pragma unroll
+      for (int i = 0; i < WT; ++i) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          slot4(i * DT + dt) = make_float4(acc[i][dt][0], acc[i][dt][1], acc[i][dt][2], acc[i][dt][3]);
+        if (Sh::WTILE) slot4(WT * DT + i) = make_float4(accw[i][0], accw[i][1], accw[i][2], accw[i][3]);
+      }
+    }
     __syncthreads();
+    if (tg == 1) return;
+#pragma unroll
+    for (int i = 0; i < WT; ++i) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const float4 o = slot4(i * DT + dt);
+        acc[i][dt] += f32x4{o.x, o.y, o.z, o.w};
+      }
+      if (Sh::WTILE) {
+        const float4 o = slot4(WT * DT + i);
+        accw[i] += f32x4{o.x, o.y, o.z, o.w};
+      }
+    }
   }
 
   // ---- partial sums: lane holds rows 4*(lane>>4)+r of column lane&15 per tile
@@ -999,17 +1072,17 @@ bool part_ok(const SegParams& p, int mode, const PartParams* pp, int& nvec, int&
 
 constexpr int MSUBT = 32;   // tokens per sub-chunk of the MFMA kernel
 
-template <typename T, int DP, int MODE, int NV>
+template <typename T, int DP, int MODE, int NV, int TG>
 hipError_t launch_mma(const SegParams& p, const PartParams& pp, int stage, hipStream_t st) {
-  using Sh = MmaShape<DP, MODE, NV, MSUBT>;
+  using Sh = MmaShape<DP, MODE, NV, MSUBT, TG>;
   const int BH = p.B * p.H;
   if (stage == 0) {
-    const void* fn = reinterpret_cast<const void*>(&seg_mma_kernel<T, DP, MODE, NV, MSUBT>);
+    const void* fn = reinterpret_cast<const void*>(&seg_mma_kernel<T, DP, MODE, NV, MSUBT, TG>);
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Sh::LDS);
     if (e != hipSuccess) return e;
     const int nsg = (p.M + Sh::MS - 1) / Sh::MS;
     dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk * nsg);
-    hipLaunchKernelGGL((seg_mma_kernel<T, DP, MODE, NV, MSUBT>), grid, dim3(Sh::THREADS), Sh::LDS, st, p, pp);
+    hipLaunchKernelGGL((seg_mma_kernel<T, DP, MODE, NV, MSUBT, TG>), grid, dim3(Sh::THREADS), Sh::LDS, st, p, pp);
   } else {
     const int G = (p.M + GS - 1) / GS;
     hipLaunchKernelGGL((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G),
@@ -1023,9 +1096,17 @@ template <typename T, int DP>
 hipError_t launch_seg_t(const SegParams& p, int mode, const PartParams* pp, int stage, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     if (!pp || pp->nchunk <= 0 || pp->chunk_tokens % MSUBT != 0) return hipErrorInvalidValue;
-    if (mode == SEG_ATTBWD) return launch_mma<T, DP, SEG_ATTBWD, 2>(p, *pp, stage, st);
-    if (p.b_same_as_a) return launch_mma<T, DP, SEG_UPDATE, 1>(p, *pp, stage, st);
-    return launch_mma<T, DP, SEG_UPDATE, 2>(p, *pp, stage, st);
+    if (mode == SEG_ATTBWD) return launch_mma<T, DP, SEG_ATTBWD, 2, 1>(p, *pp, stage, st);
+    // Update with one vector: blocks of two token groups over pairs of the
+    // carved chunks (same waves per CU, half the partials to write and add).
+    // Both stages see the paired chunking.
+    if (p.b_same_as_a) {
+      PartParams q = *pp;
+      q.nchunk = (pp->nchunk + 1) / 2;
+      q.chunk_tokens = pp->chunk_tokens * 2;
+      return launch_mma<T, DP, SEG_UPDATE, 1, 2>(p, q, stage, st);
+    }
+    return launch_mma<T, DP, SEG_UPDATE, 2, 1>(p, *pp, stage, st);
   } else {
     int nvec, MS;
     size_t lds;
