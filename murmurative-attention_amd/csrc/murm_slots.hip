@@ -51,9 +51,27 @@ __device__ __forceinline__ bool seg_block(const SegParams& p, int& bh, int& g0) 
 // Epilogues of the chunk reduction.  The
 // block holds, in LDS, the sums of rows lo .. lo+NS-1 (lo = g0 - halo).
 // ---------------------------------------------------------------------------
+// The old state of the rows a thread visits first in the update epilogue's
+// EMA loop (loaded at kernel start, before the partials).
+struct OldState {
+  float k[2], v[2];
+};
+
+__device__ __forceinline__ void load_old(const SegParams& p, int bh, int lo, int NS, int DP, OldState& os) {
+  const int64_t base = (int64_t)bh * p.M * p.D;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int i = threadIdx.x + e * blockDim.x;
+    const int rel = i / DP, d = i % DP, m = lo + rel;
+    const bool ok = p.sk_new && i < NS * DP && m >= 0 && m < p.M && d < p.D;
+    os.k[e] = ok ? p.sk_old[base + (int64_t)m * p.D + d] : 0.f;
+    os.v[e] = ok ? p.sv_old[base + (int64_t)m * p.D + d] : 0.f;
+  }
+}
+
 template <int DP>
 __device__ void update_epilogue(const SegParams& p, int bh, int g0, int halo, int NS, float* accA, float* accB,
-                                const float* accW) {
+                                const float* accW, const OldState& os) {
   const int lo = g0 - halo;
   const int64_t base = (int64_t)bh * p.M * p.D;
   const float a = p.alpha, oma = 1.0f - p.alpha;
@@ -69,12 +87,12 @@ __device__ void update_epilogue(const SegParams& p, int bh, int g0, int halo, in
   if (!p.sk_new) return;
   __syncthreads();
   // EMA on every row the block holds (owned + halo)
-  for (int i = threadIdx.x; i < NS * DP; i += blockDim.x) {
+  for (int i = threadIdx.x, e = 0; i < NS * DP; i += blockDim.x, ++e) {
     const int rel = i / DP, d = i % DP, m = lo + rel;
     if (m < 0 || m >= p.M || d >= p.D) continue;
     const float W = accW[rel];
-    const float ok = p.sk_old[base + (int64_t)m * p.D + d];
-    const float ov = p.sv_old[base + (int64_t)m * p.D + d];
+    const float ok = e == 0 ? os.k[0] : (e == 1 ? os.k[1] : p.sk_old[base + (int64_t)m * p.D + d]);
+    const float ov = e == 0 ? os.v[0] : (e == 1 ? os.v[1] : p.sv_old[base + (int64_t)m * p.D + d]);
     if (W > 0.f) {
       const float inv = 1.0f / (W + p.eps);
       accA[i] = a * ok + oma * (accA[i] * inv);
@@ -100,19 +118,35 @@ __device__ void update_epilogue(const SegParams& p, int bh, int g0, int halo, in
   }
 }
 
+// The previous round's forward sums of the slot a thread's 32-lane group owns
+// first in the epilogue (loaded at kernel start, before the partials).
 template <int DP>
-__device__ void attbwd_epilogue(const SegParams& p, int bh, int g0, int halo, int NS, float* accA, float* accB) {
-  const int lo = g0 - halo;
+struct PrevSums {
+  float W;
+  float k[DP / 32], v[DP / 32];
+};
+
+template <int DP>
+__device__ __forceinline__ void load_prev(const SegParams& p, int bh, int g0, PrevSums<DP>& ps) {
+  constexpr int DPT = DP / 32;
+  const int own = threadIdx.x >> 5, sub = threadIdx.x & 31, m = g0 + own;
+  const bool live = own < GS && m < p.M;
   const int64_t base = (int64_t)bh * p.M * p.D;
-  // G'' rows (owned + halo)
-  for (int i = threadIdx.x; i < NS * DP; i += blockDim.x) {
-    const int rel = i / DP, d = i % DP, m = lo + rel;
-    if (m < 0 || m >= p.M || d >= p.D) continue;
-    const int64_t o = base + (int64_t)m * p.D + d;
-    accA[i] += p.carry_k ? p.carry_k[o] : 0.f;
-    accB[i] += p.carry_v ? p.carry_v[o] : 0.f;
+  ps.W = live ? p.Wp[(int64_t)bh * p.M + m] : 0.f;
+#pragma unroll
+  for (int t = 0; t < DPT; ++t) {
+    const int d = sub + 32 * t;
+    const bool ok = live && d < p.D;
+    ps.k[t] = ok ? p.Kp[base + (int64_t)m * p.D + d] : 0.f;
+    ps.v[t] = ok ? p.Vp[base + (int64_t)m * p.D + d] : 0.f;
   }
-  __syncthreads();
+}
+
+// accA / accB hold G'' (chunk sums + carry) of the owned and halo rows.
+template <int DP>
+__device__ void attbwd_epilogue(const SegParams& p, int bh, int g0, int halo, int NS, float* accA, float* accB,
+                                const PrevSums<DP>& ps) {
+  const int64_t base = (int64_t)bh * p.M * p.D;
   if (p.final_out) {
     const int b = bh / p.H, h = bh % p.H;
     for (int i = threadIdx.x; i < GS * DP; i += blockDim.x) {
@@ -148,7 +182,8 @@ __device__ void attbwd_epilogue(const SegParams& p, int bh, int g0, int halo, in
   for (int own = threadIdx.x >> 5; own < GS; own += blockDim.x >> 5) {
     const int m = g0 + own, rel = own + halo;
     const bool live = m < p.M;
-    const float W = live ? p.Wp[(int64_t)bh * p.M + m] : 0.f;
+    const bool first = own == (int)(threadIdx.x >> 5);  // prefetched
+    const float W = first ? ps.W : (live ? p.Wp[(int64_t)bh * p.M + m] : 0.f);
     const bool used = W > 0.f;
     const float inv = oma / (W + p.eps);
     float dot = 0.f;
@@ -166,7 +201,7 @@ __device__ void attbwd_epilogue(const SegParams& p, int bh, int g0, int halo, in
       };
       const float gk = adj(accA), gv = adj(accB);
       const int64_t o = base + (int64_t)m * p.D + d;
-      if (used) dot += p.Kp[o] * gk + p.Vp[o] * gv;
+      if (used) dot += (first ? ps.k[t] : p.Kp[o]) * gk + (first ? ps.v[t] : p.Vp[o]) * gv;
       const float dk = used ? inv * gk : 0.f, dv = used ? inv * gv : 0.f;
       if (p.combine_dk) {
         p.dk_out[o] = dk + dv;
@@ -815,6 +850,10 @@ __global__ __launch_bounds__(RED_THREADS) void seg_reduce_kernel(SegParams p, Pa
   // adding them in chunk order.
   const int nquad = nv * NS * QPR;
   const int nitem = nquad + (MODE == SEG_UPDATE ? NS : 0);
+  PrevSums<DP> ps{};
+  OldState os{};
+  if (MODE == SEG_ATTBWD && !p.final_out) load_prev<DP>(p, bh, g0, ps);  // in flight with the partials
+  if (MODE == SEG_UPDATE) load_old(p, bh, lo, NS, DP, os);
   for (int i = threadIdx.x; i < nitem; i += blockDim.x) {
     if (i >= nquad) {
       const int rel = i - nquad, m = lo + rel;
@@ -838,7 +877,11 @@ __global__ __launch_bounds__(RED_THREADS) void seg_reduce_kernel(SegParams p, Pa
     float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
     if (m >= 0 && m < p.M && d < p.D) {
       const float* src = (v == 0 ? pp.partA : pp.partB) + ((int64_t)bh * p.M + m) * p.D + d;
+      // ATTBWD: the carried gradient of the row is added after the chunk sums
+      const float* cry = MODE == SEG_ATTBWD ? (v == 0 ? p.carry_k : p.carry_v) : nullptr;
+      const int64_t co = ((int64_t)bh * p.M + m) * p.D + d;
       if ((p.D & 3) == 0) {
+        const float4 cv = cry ? *reinterpret_cast<const float4*>(cry + co) : make_float4(0.f, 0.f, 0.f, 0.f);
         for (int c0 = 0; c0 < nc; c0 += NCB) {  // chunk order: batches of NCB loads in flight
           float4 x[NCB];
 #pragma unroll
@@ -852,11 +895,15 @@ __global__ __launch_bounds__(RED_THREADS) void seg_reduce_kernel(SegParams p, Pa
             }
           }
         }
+        if (cry) { sum.x += cv.x; sum.y += cv.y; sum.z += cv.z; sum.w += cv.w; }
       } else {
         float t[4] = {0.f, 0.f, 0.f, 0.f};
         for (int c = 0; c < nc; ++c)
           for (int e = 0; e < 4; ++e)
             if (d + e < p.D) t[e] += src[c * cstride + e];
+        if (cry)
+          for (int e = 0; e < 4; ++e)
+            if (d + e < p.D) t[e] += cry[co + e];
         sum = make_float4(t[0], t[1], t[2], t[3]);
       }
     }
@@ -869,9 +916,9 @@ __global__ __launch_bounds__(RED_THREADS) void seg_reduce_kernel(SegParams p, Pa
   }
   __syncthreads();
   if (MODE == SEG_UPDATE)
-    update_epilogue<DP>(p, bh, g0, halo, NS, accA, accB, accW);
+    update_epilogue<DP>(p, bh, g0, halo, NS, accA, accB, accW, os);
   else
-    attbwd_epilogue<DP>(p, bh, g0, halo, NS, accA, accB);
+    attbwd_epilogue<DP>(p, bh, g0, halo, NS, accA, accB, ps);
 }
 
 // One block per (b,h): G' = D^T G'' (optional), then the EMA backward.
