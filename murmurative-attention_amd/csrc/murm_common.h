@@ -258,6 +258,29 @@ constexpr int table_stride() { return DP == 64 ? 64 : DP + 4; }
 template <int DP>
 __device__ __forceinline__ int tok_swap() { return DP == 64 ? (int)((threadIdx.x >> 3) & 1) : 0; }
 
+// Slot j of a raw index row (8 u16 in one 16-byte load).
+__device__ __forceinline__ uint32_t idx_at(const uint4& r, int j) {
+  const uint32_t w = j < 2 ? r.x : (j < 4 ? r.y : (j < 6 ? r.z : r.w));
+  return (w >> (16 * (j & 1))) & 0xFFFF;
+}
+
+// One row of KN = 7 floats (28 bytes, 4-byte aligned) with two vector
+// accesses (16 + 12 bytes); global memory takes unaligned vector accesses.
+__device__ __forceinline__ void load_row7(const float* src, float (&v)[KN]) {
+  float4 a;
+  float3 c;
+  __builtin_memcpy(&a, src, 16);
+  __builtin_memcpy(&c, src + 4, 12);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = c.x; v[5] = c.y; v[6] = c.z;
+}
+__device__ __forceinline__ void store_row7(float* dst, const float (&v)[KN]) {
+  const float4 a = make_float4(v[0], v[1], v[2], v[3]);
+  const float3 c = make_float3(v[4], v[5], v[6]);
+  __builtin_memcpy(dst, &a, 16);
+  __builtin_memcpy(dst + 4, &c, 12);
+}
+
 // Global -> LDS copy of `bytes` contiguous bytes (a multiple of 16; both
 // ends 16-byte aligned) without a trip through registers: each wave issues
 // global_load_lds_dwordx4 for its 1 KiB pieces (lane l's 16 bytes land at the

@@ -29,11 +29,6 @@ namespace {
 
 constexpr int GS = 16;                 // owned slots per block
 constexpr int NSMAX = GS + 2;          // with halo
-__device__ __forceinline__ uint32_t idx_at(const uint4& r, int j) {
-  const uint32_t w = j < 2 ? r.x : (j < 4 ? r.y : (j < 6 ? r.z : r.w));
-  return (w >> (16 * (j & 1))) & 0xFFFF;
-}
-
 // 1-D grid, XCD-aware: workgroups are dispatched round-robin over the 8 XCDs
 // (linear id % 8), so every block of one (b,h) is placed on XCD bh % 8 and
 // reads what the head's other blocks wrote or staged from that XCD's L2.

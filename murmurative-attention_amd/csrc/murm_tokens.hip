@@ -14,6 +14,7 @@
 // gradient once instead of read-modify-writing it every round.
 
 #include <initializer_list>
+#include <type_traits>
 
 #include "murm_common.h"
 #include "murm_launch.h"
@@ -314,69 +315,94 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParam
   for (int q = 0; q < PK; ++q)
 #pragma unroll
     for (int i = 0; i < 8; ++i) { ak[q][i] = 0.f; av[q][i] = 0.f; }
+  // next pass's index row (raw), weights and softmax grads, requested before
+  // the current pass's gathers
+  uint4 irn;
+  float wn[KN], dn[KN];
   for (int r = 0; r < p.R; ++r) {
-    const bool use_sk = p.ds[r] && p.dq.p;
+    const uint16_t* idx_r = p.idx[r];
+    const float* w_r = p.w[r];
+    const float* ds_r = p.ds[r];
+    const float* dkk_r = p.dkk[r];
+    const float* dkv_r = p.dkv[r];
+    const bool use_sk = ds_r && p.dq.p;
     float* tsk = t0;
     float* tdk = tsk + (use_sk ? p.M * RSD : 0);
-    float* tdv = tdk + (p.dkk[r] ? p.M * RSD : 0);
+    float* tdv = tdk + (dkk_r ? p.M * RSD : 0);
     if (r > 0) __syncthreads();  // the previous round's tables are no longer read
     if (use_sk) stage_table<DP>(tsk, p.sk[r] + tb, p.M, p.D);
-    if (p.dkk[r]) stage_table<DP>(tdk, p.dkk[r] + tb, p.M, p.D);
-    if (p.dkv[r]) stage_table<DP>(tdv, p.dkv[r] + tb, p.M, p.D);
+    if (dkk_r) stage_table<DP>(tdk, dkk_r + tb, p.M, p.D);
+    if (dkv_r) stage_table<DP>(tdv, dkv_r + tb, p.M, p.D);
     __syncthreads();
-    // index rows, weights and softmax grads of pass q+1 are requested before
-    // pass q's gathers
-    uint32_t sln[KN];
-    float wn[KN], dn[KN];
-    auto fetch = [&](int q) {
-      const int n = min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1);
-      const int64_t row = (int64_t)bh * p.N + n;
-      unpack_idx(p.idx[r] + row * IDX_ROW, sln);
+    // the round's passes, specialised on which tables it has
+    auto passes = [&](auto sk_c, auto dk_c, auto dv_c) {
+      constexpr bool SK = decltype(sk_c)::value, DK = decltype(dk_c)::value, DV = decltype(dv_c)::value;
+      auto fetch = [&](int q) {
+        const int n = min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1);
+        const int64_t row = (int64_t)bh * p.N + n;
+        irn = *reinterpret_cast<const uint4*>(idx_r + row * IDX_ROW);
+        load_row7(w_r + row * KN, wn);
+        if (SK) load_row7(ds_r + row * KN, dn);
+      };
+      fetch(0);
 #pragma unroll
-      for (int j = 0; j < KN; ++j) {
-        wn[j] = p.w[r][row * KN + j];
-        dn[j] = use_sk ? p.ds[r][row * KN + j] : 0.f;
+      for (int q = 0; q < PASSES; ++q) {
+        const uint4 ir = irn;
+        float wr[KN], dsr[KN];
+#pragma unroll
+        for (int j = 0; j < KN; ++j) { wr[j] = wn[j]; dsr[j] = SK ? dn[j] : 0.f; }
+        if (q + 1 < PASSES) fetch(q + 1);
+        const int n = c_beg + q * TPP + threadIdx.x / DCH;
+        if (n >= p.N) continue;
+        // rows of slot j + 1 are read while slot j's are accumulated; the
+        // scheduling barrier keeps the compiler from reading further ahead
+        // (all 7 slots' rows in flight would double the registers)
+        float vs[2][8], vk[2][8], vv[2][8];
+        auto rows = [&](int j, int o) {
+          const uint32_t sl = idx_at(ir, j);
+          if constexpr (SK) lds8s<DP>(tsk + sl * RSD, dc, sw, vs[o]);
+          if constexpr (DK) lds8s<DP>(tdk + sl * RSD, dc, sw, vk[o]);
+          if constexpr (KV && DV) lds8s<DP>(tdv + sl * RSD, dc, sw, vv[o]);
+        };
+        rows(0, 0);
+#pragma unroll
+        for (int j = 0; j < KN; ++j) {
+          const int o = j & 1;
+          if (j + 1 < KN) rows(j + 1, o ^ 1);
+          if constexpr (SK) {
+            const float cj = p.c * dsr[j];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) aq[q][i] += cj * vs[o][i];
+          }
+          const float wj = wr[j];
+          if constexpr (DK) {
+            if constexpr (KV) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) ak[q][i] += wj * vk[o][i];
+            } else {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) aq[q][i] += wj * vk[o][i];
+            }
+          }
+          if constexpr (KV && DV) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) av[q][i] += wj * vv[o][i];
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     };
-    fetch(0);
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      uint32_t sl[KN];
-      float wr[KN], dsr[KN];
-#pragma unroll
-      for (int j = 0; j < KN; ++j) { sl[j] = sln[j]; wr[j] = wn[j]; dsr[j] = dn[j]; }
-      if (q + 1 < PASSES) fetch(q + 1);
-      const int n = c_beg + q * TPP + threadIdx.x / DCH;
-      if (n >= p.N) continue;
-#pragma unroll
-      for (int j = 0; j < KN; ++j) {
-        float v[8];
-        if (use_sk) {
-          const float cj = p.c * dsr[j];
-          lds8s<DP>(tsk + sl[j] * RSD, dc, sw, v);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) aq[q][i] += cj * v[i];
-        }
-        const float wj = wr[j];
-        if (p.dkk[r]) {
-          lds8s<DP>(tdk + sl[j] * RSD, dc, sw, v);
-          if constexpr (KV) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) ak[q][i] += wj * v[i];
-          } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) aq[q][i] += wj * v[i];
-          }
-        }
-        if constexpr (KV) {
-          if (p.dkv[r]) {
-            lds8s<DP>(tdv + sl[j] * RSD, dc, sw, v);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) av[q][i] += wj * v[i];
-          }
-        }
+    using Y = std::true_type;
+    using N_ = std::false_type;
+    if constexpr (KV) {
+      if (dkv_r) {
+        if (use_sk) { if (dkk_r) passes(Y{}, Y{}, Y{}); else passes(Y{}, N_{}, Y{}); }
+        else { if (dkk_r) passes(N_{}, Y{}, Y{}); else passes(N_{}, N_{}, Y{}); }
+        continue;
       }
     }
+    if (use_sk) { if (dkk_r) passes(Y{}, Y{}, N_{}); else passes(Y{}, N_{}, N_{}); }
+    else if (dkk_r) passes(N_{}, Y{}, N_{});
   }
 #pragma unroll
   for (int q = 0; q < PASSES; ++q) {
