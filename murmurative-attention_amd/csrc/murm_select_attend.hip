@@ -83,12 +83,13 @@ __device__ __forceinline__ void write_token(const SAParams& p, int bh, int n, co
     r.w = slot[6] | ((uint32_t)IDX_NONE << 16);
     *reinterpret_cast<uint4*>(p.idx16 + row * IDX_ROW) = r;
   }
-  if (p.idx64) {
+  if (p.idx64) {  // 56 bytes, 8-byte aligned: vector stores
+    int64_t v[KN];
 #pragma unroll
-    for (int j = 0; j < KN; ++j) p.idx64[row * KN + j] = (int64_t)slot[j];
+    for (int j = 0; j < KN; ++j) v[j] = (int64_t)slot[j];
+    __builtin_memcpy(p.idx64 + row * KN, v, sizeof(v));
   }
-#pragma unroll
-  for (int j = 0; j < KN; ++j) p.w[row * KN + j] = w[j];
+  store_row7(p.w + row * KN, w);
 }
 
 // Raw 8-element load of a 16-bit token row into an MFMA operand (zero fill).
@@ -520,8 +521,7 @@ __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p,
       const int n = min(c_beg + q * TPP + (int)threadIdx.x / DCH, p.N - 1);
       const int64_t row = (int64_t)bh * p.N + n;
       ix[q] = *reinterpret_cast<const uint4*>(p.rp.idx[r] + row * IDX_ROW);
-#pragma unroll
-      for (int j = 0; j < KN; ++j) wv[q][j] = p.rp.w[r][row * KN + j];
+      load_row7(p.rp.w[r] + row * KN, wv[q]);
     }
     if (r > 0) __syncthreads();
     stage_table<DP>(tab, p.rp.a[r] + (int64_t)bh * p.M * p.D, p.M, p.D);

@@ -220,6 +220,9 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
   if (p.dW)
     for (int i = threadIdx.x; i < p.M; i += blockDim.x) tdw[i] = p.dW[(int64_t)bh * p.M + i];
   __syncthreads();
+  // the passes, specialised on which tables are present
+  auto passes = [&](auto g_c, auto k_c) {
+  constexpr bool HG = decltype(g_c)::value, HK = decltype(k_c)::value;
 #pragma unroll
   for (int q = 0; q < NP; ++q) {
     const int n = c_beg + q * TPP + threadIdx.x / DCH;
@@ -227,29 +230,38 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
     const uint32_t sl[KN] = {ir.x & 0xFFFF, ir.x >> 16, ir.y & 0xFFFF, ir.y >> 16,
                              ir.z & 0xFFFF, ir.z >> 16, ir.w & 0xFFFF};
     float g[8], a[8], c[8];
-    if (has_g) unraw8s<T, DP>(rg[q], g, dc, sw, p.D);
-    if (has_k) unraw8s<T, DP>(rk[q], a, dc, sw, p.D);
+    if constexpr (HG) unraw8s<T, DP>(rg[q], g, dc, sw, p.D);
+    if constexpr (HK) unraw8s<T, DP>(rk[q], a, dc, sw, p.D);
     if constexpr (HV) unraw8s<T, DP>(rv[q], c, dc, sw, p.D);
     float dw[KN];
+    // rows of slot j + 1 are read while slot j's are used; the scheduling
+    // barrier keeps the compiler from reading further ahead
+    float vs[2][8], vk[2][8], vv[2][8];
+    auto rows = [&](int j, int o) {
+      if constexpr (HG) lds8s<DP>(tsv + sl[j] * RSD, dc, sw, vs[o]);
+      if constexpr (HK) lds8s<DP>(tdk + sl[j] * RSD, dc, sw, vk[o]);
+      if constexpr (HV) lds8s<DP>(tdv + sl[j] * RSD, dc, sw, vv[o]);
+    };
+    rows(0, 0);
 #pragma unroll
     for (int j = 0; j < KN; ++j) {
-      float sacc = 0.f, v[8];
-      if (has_g) {
-        lds8s<DP>(tsv + sl[j] * RSD, dc, sw, v);
+      const int o = j & 1;
+      if (j + 1 < KN) rows(j + 1, o ^ 1);
+      float sacc = 0.f;
+      if constexpr (HG) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) sacc += g[i] * v[i];
+        for (int i = 0; i < 8; ++i) sacc += g[i] * vs[o][i];
       }
-      if (has_k) {
-        lds8s<DP>(tdk + sl[j] * RSD, dc, sw, v);
+      if constexpr (HK) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) sacc += a[i] * v[i];
+        for (int i = 0; i < 8; ++i) sacc += a[i] * vk[o][i];
       }
       if constexpr (HV) {
-        lds8s<DP>(tdv + sl[j] * RSD, dc, sw, v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) sacc += c[i] * v[i];
+        for (int i = 0; i < 8; ++i) sacc += c[i] * vv[o][i];
       }
       dw[j] = group_sum<DCH>(sacc);
+      __builtin_amdgcn_sched_barrier(0);
     }
     // lane dc finishes weights j = dc, dc + DCH, ...
     float mine[JPL];
@@ -279,6 +291,11 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
       if (p.ds_out) p.ds_out[row * KN + jj] = wq[q][u] * (mine[u] - dot);
     }
   }
+  };
+  using Y = std::true_type;
+  using N_ = std::false_type;
+  if (has_g) { if (has_k) passes(Y{}, Y{}); else passes(Y{}, N_{}); }
+  else { if (has_k) passes(N_{}, Y{}); else passes(N_{}, N_{}); }
 }
 
 // tok_grad with each round's tables staged in LDS in turn; a thread keeps the
