@@ -286,7 +286,7 @@ __device__ __forceinline__ void store_row7(float* dst, const float (&v)[KN]) {
 // global_load_lds_dwordx4 for its 1 KiB pieces (lane l's 16 bytes land at the
 // piece's LDS base + 16 l), all pieces in flight at once, then waits for
 // them.  The caller's barrier publishes the copy to the other waves.
-__device__ __forceinline__ void copy_to_lds(void* dst, const void* src, int bytes) {
+__device__ __forceinline__ void issue_copy_to_lds(void* dst, const void* src, int bytes) {
   typedef __attribute__((address_space(3))) void* lds_ptr;
   typedef __attribute__((address_space(1))) void* glb_ptr;
   const int lane = threadIdx.x & 63;
@@ -297,14 +297,24 @@ __device__ __forceinline__ void copy_to_lds(void* dst, const void* src, int byte
     if (o < bytes)
       __builtin_amdgcn_global_load_lds((glb_ptr)((const char*)src + o), (lds_ptr)((char*)dst + off), 16, 0, 0);
   }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's pieces are in LDS
+}
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+__device__ __forceinline__ void copy_to_lds(void* dst, const void* src, int bytes) {
+  issue_copy_to_lds(dst, src, bytes);
+  wait_vm();  // this wave's pieces are in LDS
+}
+// A table of M rows of D floats at `src` is copied to LDS as it lies
+// (unpadded rows of the full width, 16-byte aligned source).
+template <int DP>
+__device__ __forceinline__ bool table_direct(const float* src, int D) {
+  return table_stride<DP>() == D && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
 }
 
 template <int DP>
 __device__ __forceinline__ void stage_table(float* __restrict__ dst, const float* __restrict__ src, int M, int D) {
   constexpr int RSD = table_stride<DP>();
   // unpadded rows of the full width: the LDS table is the global one
-  if (RSD == D && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+  if (table_direct<DP>(src, D)) {
     copy_to_lds(dst, src, M * D * 4);
     return;
   }
