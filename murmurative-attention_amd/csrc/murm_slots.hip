@@ -496,7 +496,10 @@ struct MmaShape {
   static constexpr int WT = 256 / DP;                       // slot tiles per wave: 64 accumulators
   static constexpr int ROWB = SUBT * 2;
   static constexpr int MS_REG = MMA_WAVES * WT * 16;
-  static constexpr int MS_LDS = (64 * 1024) / (KINDS * 2 * ROWB);  // C^T within 64 KiB
+  // C^T in what is left of 144 KiB (per token group) after the token rows,
+  // in whole groups of MMA_WAVES tiles
+  static constexpr int MS_LDS =
+      (((144 * 1024) / TG - NV * DP * ROWB) / (KINDS * 2 * ROWB)) / (MMA_WAVES * 16) * (MMA_WAVES * 16);
   static constexpr int MS = MS_REG < MS_LDS ? MS_REG : MS_LDS;    // slots per block
   static constexpr size_t GLDS = (size_t)NV * DP * ROWB + (size_t)KINDS * 2 * MS * ROWB;  // per group
   static constexpr int NACC = WT * DT + WTILE * WT;         // float4 accumulators per thread
@@ -1112,7 +1115,9 @@ bool part_ok(const SegParams& p, int mode, const PartParams* pp, int& nvec, int&
   return pp && pp->nchunk > 0 && lds <= 160 * 1024;
 }
 
-constexpr int MSUBT = 32;   // tokens per sub-chunk of the MFMA kernel
+// Tokens per sub-chunk of the MFMA kernel: 64 halves the barrier rounds of
+// 32 (and the sub-chunk's staging latency per token) within the LDS budget.
+constexpr int MSUBT = 64;
 
 template <typename T, int DP, int MODE, int NV, int TG>
 hipError_t launch_mma(const SegParams& p, const PartParams& pp, int stage, hipStream_t st) {
