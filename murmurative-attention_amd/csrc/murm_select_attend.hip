@@ -109,7 +109,7 @@ __device__ __forceinline__ V load_operand8(const T* row, int d0, int D, bool vec
 // ---------------------------------------------------------------------------
 // 16-bit tokens (bf16 / fp16): hi/lo split keys in LDS, 16x16x32 MFMA
 // ---------------------------------------------------------------------------
-template <typename T, int DP>
+template <typename T, int DP, bool WIDE>
 __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
   using V = typename Mfma16<T>::vec;
   constexpr int G = SAShape<DP>::G;
@@ -123,6 +123,24 @@ __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
   const int bh = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
   const float* skb = p.sk + (int64_t)bh * p.M * p.D;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int quad = lane >> 4, col = lane & 15;
+  const int tok0 = blockIdx.x * SAShape<DP, SA16_WAVES>::TOK + wave * (G * 16);
+
+  // WIDE (16-byte aligned rows, D % 8 == 0): the wave's token rows are
+  // requested before the keys are staged, unconditionally from clamped rows
+  // and units, and zeroed where out of range only after the staging
+  uint4 rq[G][KC];
+  if constexpr (WIDE) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const T* row = tok_row<T>(p.q, b, h, min(tok0 + 16 * g + col, p.N - 1));
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+        rq[g][kc] = *reinterpret_cast<const uint4*>(row + min(32 * kc + 8 * quad, p.D - 8));
+    }
+  }
 
   // stage the keys: batches of STB float4 loads in flight per thread, then
   // the hi/lo split written as 8-byte LDS stores
@@ -166,20 +184,20 @@ __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
   }
   __syncthreads();
 
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int quad = lane >> 4, col = lane & 15;
-  const int tok0 = blockIdx.x * SAShape<DP, SA16_WAVES>::TOK + wave * (G * 16);
   if (tok0 >= p.N) return;  // whole wave past the end (no block-wide sync below)
 
   V bq[G][KC];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int n = tok0 + 16 * g + col;
-    const T* row = tok_row<T>(p.q, b, h, n < p.N ? n : 0);
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      bq[g][kc] = load_operand8<T, V>(row, 32 * kc + 8 * quad, p.D, p.q.vec);
+      if constexpr (WIDE) {
+        bq[g][kc] = *reinterpret_cast<const V*>(&rq[g][kc]);
+        if (32 * kc + 8 * quad >= p.D) bq[g][kc] = V{};
+      } else {
+        bq[g][kc] = load_operand8<T, V>(tok_row<T>(p.q, b, h, n < p.N ? n : 0), 32 * kc + 8 * quad, p.D, false);
+      }
       if (n >= p.N) bq[g][kc] = V{};
     }
   }
@@ -555,10 +573,15 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
     dim3 grid((p.N + S::TOK - 1) / S::TOK, p.B * p.H);
     const size_t lds = 2 * (size_t)Mp * (DP + 8) * sizeof(T);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sa_kernel16<T, DP>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const bool wide = p.q.vec && p.D % 8 == 0;
+    const void* fn = wide ? reinterpret_cast<const void*>(&sa_kernel16<T, DP, true>)
+                          : reinterpret_cast<const void*>(&sa_kernel16<T, DP, false>);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((sa_kernel16<T, DP>), grid, dim3(64 * SA16_WAVES), lds, st, p);
+    if (wide)
+      hipLaunchKernelGGL((sa_kernel16<T, DP, true>), grid, dim3(64 * SA16_WAVES), lds, st, p);
+    else
+      hipLaunchKernelGGL((sa_kernel16<T, DP, false>), grid, dim3(64 * SA16_WAVES), lds, st, p);
   } else {
     dim3 grid((p.N + SAShape<DP>::TOK - 1) / SAShape<DP>::TOK, p.B * p.H);
     const size_t lds = (size_t)Mp * (DP + 4) * sizeof(float);
