@@ -983,6 +983,50 @@ __global__ void to_state_kernel(SlotConv<const T*, float*> c0, SlotConv<const T*
   }
 }
 
+// The same with one thread per 4 consecutive elements of a row and 32-bit
+// index arithmetic (B*H*M*ceil(D/4) < 2^30; the launchers check).
+template <typename T>
+__global__ void to_state4_kernel(SlotConv<const T*, float*> c0, SlotConv<const T*, float*> c1, int H, int M,
+                                 int D, int total4) {
+  const SlotConv<const T*, float*>& c = blockIdx.y == 0 ? c0 : c1;
+  const int D4 = (D + 3) >> 2;
+  for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < total4; q += gridDim.x * blockDim.x) {
+    const int row = q / D4, d0 = (q - row * D4) * 4;
+    const int bh = row / M, m = row - bh * M, b = bh / H, h = bh - b * H;
+    const T* sp = c.src + b * c.sb + h * c.sh + (int64_t)m * c.sm + d0;
+    float* o = c.dst + (int64_t)row * D + d0;
+    if (d0 + 4 <= D) {
+      const float4 v = make_float4(to_f(sp[0]), to_f(sp[1]), to_f(sp[2]), to_f(sp[3]));
+      if ((D & 3) == 0) {
+        *reinterpret_cast<float4*>(o) = v;
+      } else {
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+      }
+    } else {
+      for (int e = 0; d0 + e < D; ++e) o[e] = to_f(sp[e]);
+    }
+  }
+}
+
+template <typename T>
+__global__ void from_state4_kernel(SlotConv<const float*, T*> c0, SlotConv<const float*, T*> c1, int H, int M,
+                                   int D, int total4) {
+  const SlotConv<const float*, T*>& c = blockIdx.y == 0 ? c0 : c1;
+  const int D4 = (D + 3) >> 2;
+  for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < total4; q += gridDim.x * blockDim.x) {
+    const int row = q / D4, d0 = (q - row * D4) * 4;
+    const int bh = row / M, m = row - bh * M, b = bh / H, h = bh - b * H;
+    const float* sp = c.src + (int64_t)row * D + d0;
+    T* o = c.dst + b * c.sb + h * c.sh + (int64_t)m * c.sm + d0;
+    if (d0 + 4 <= D) {
+      const float4 v = (D & 3) == 0 ? *reinterpret_cast<const float4*>(sp) : make_float4(sp[0], sp[1], sp[2], sp[3]);
+      o[0] = from_f<T>(v.x); o[1] = from_f<T>(v.y); o[2] = from_f<T>(v.z); o[3] = from_f<T>(v.w);
+    } else {
+      for (int e = 0; d0 + e < D; ++e) o[e] = from_f<T>(sp[e]);
+    }
+  }
+}
+
 template <typename T>
 __global__ void from_state_kernel(SlotConv<const float*, T*> c0, SlotConv<const float*, T*> c1, int B, int H,
                                   int M, int D) {
@@ -1223,12 +1267,29 @@ hipError_t launch_du(const DuParams& p, hipStream_t st) {
 
 hipError_t launch_to_state2(int dtype, const SlotConv<const void*, float*>& a,
                             const SlotConv<const void*, float*>* bp, int B, int H, int M, int D, hipStream_t st) {
-  const dim3 grid(grid1d((int64_t)B * H * M * D), bp ? 2 : 1);
   const SlotConv<const void*, float*> bb = bp ? *bp : a;
   auto cv = [](const SlotConv<const void*, float*>& c, auto* tag) {
     using T = std::remove_const_t<std::remove_pointer_t<decltype(tag)>>;
     return SlotConv<const T*, float*>{static_cast<const T*>(c.src), c.sb, c.sh, c.sm, c.dst};
   };
+  const int64_t total4 = (int64_t)B * H * M * ((D + 3) / 4);
+  if (total4 < (int64_t(1) << 30)) {  // 32-bit indices, grid-stride step included
+    const dim3 g4(grid1d(total4), bp ? 2 : 1);
+    switch (dtype) {
+      case DT_BF16: hipLaunchKernelGGL((to_state4_kernel<__bf16>), g4, dim3(256), 0, st,
+                                       cv(a, (const __bf16*)nullptr), cv(bb, (const __bf16*)nullptr), H, M, D,
+                                       (int)total4); break;
+      case DT_F16: hipLaunchKernelGGL((to_state4_kernel<_Float16>), g4, dim3(256), 0, st,
+                                      cv(a, (const _Float16*)nullptr), cv(bb, (const _Float16*)nullptr), H, M, D,
+                                      (int)total4); break;
+      case DT_F32: hipLaunchKernelGGL((to_state4_kernel<float>), g4, dim3(256), 0, st,
+                                      cv(a, (const float*)nullptr), cv(bb, (const float*)nullptr), H, M, D,
+                                      (int)total4); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
+  const dim3 grid(grid1d((int64_t)B * H * M * D), bp ? 2 : 1);
   switch (dtype) {
     case DT_BF16: hipLaunchKernelGGL((to_state_kernel<__bf16>), grid, dim3(256), 0, st,
                                      cv(a, (const __bf16*)nullptr), cv(bb, (const __bf16*)nullptr), B, H, M, D); break;
@@ -1244,12 +1305,27 @@ hipError_t launch_to_state2(int dtype, const SlotConv<const void*, float*>& a,
 
 hipError_t launch_from_state2(int dtype, const SlotConv<const float*, void*>& a,
                               const SlotConv<const float*, void*>* bp, int B, int H, int M, int D, hipStream_t st) {
-  const dim3 grid(grid1d((int64_t)B * H * M * D), bp ? 2 : 1);
   const SlotConv<const float*, void*> bb = bp ? *bp : a;
   auto cv = [](const SlotConv<const float*, void*>& c, auto* tag) {
     using T = std::remove_pointer_t<decltype(tag)>;
     return SlotConv<const float*, T*>{c.src, c.sb, c.sh, c.sm, static_cast<T*>(c.dst)};
   };
+  const int64_t total4 = (int64_t)B * H * M * ((D + 3) / 4);
+  if (total4 < (int64_t(1) << 30)) {  // 32-bit indices, grid-stride step included
+    const dim3 g4(grid1d(total4), bp ? 2 : 1);
+    switch (dtype) {
+      case DT_BF16: hipLaunchKernelGGL((from_state4_kernel<__bf16>), g4, dim3(256), 0, st,
+                                       cv(a, (__bf16*)nullptr), cv(bb, (__bf16*)nullptr), H, M, D, (int)total4); break;
+      case DT_F16: hipLaunchKernelGGL((from_state4_kernel<_Float16>), g4, dim3(256), 0, st,
+                                      cv(a, (_Float16*)nullptr), cv(bb, (_Float16*)nullptr), H, M, D, (int)total4);
+        break;
+      case DT_F32: hipLaunchKernelGGL((from_state4_kernel<float>), g4, dim3(256), 0, st,
+                                      cv(a, (float*)nullptr), cv(bb, (float*)nullptr), H, M, D, (int)total4); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
+  const dim3 grid(grid1d((int64_t)B * H * M * D), bp ? 2 : 1);
   switch (dtype) {
     case DT_BF16: hipLaunchKernelGGL((from_state_kernel<__bf16>), grid, dim3(256), 0, st,
                                      cv(a, (__bf16*)nullptr), cv(bb, (__bf16*)nullptr), B, H, M, D); break;
