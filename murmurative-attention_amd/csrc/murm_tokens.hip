@@ -300,8 +300,9 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
 
 // tok_grad with each round's tables staged in LDS in turn; a thread keeps the
 // gradients of its PASSES tokens in registers across the rounds.
-template <typename T, int DP, int PASSES, bool KV, bool WIDE>
+template <typename T, int DP, int PASSES, bool KV, bool WIDE, bool SEQ>
 __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParams p, int nchunk) {
+  constexpr bool seq = SEQ;
   using S = TokShape<DP>;
   constexpr int DCH = S::DCH, TPP = S::TPP, RSD = S::RSD;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -343,14 +344,17 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParam
     const float* dkk_r = p.dkk[r];
     const float* dkv_r = p.dkv[r];
     const bool use_sk = ds_r && p.dq.p;
+    // seq: the round's tables one at a time in one LDS table (they do not fit together)
     float* tsk = t0;
-    float* tdk = tsk + (use_sk ? p.M * RSD : 0);
-    float* tdv = tdk + (dkk_r ? p.M * RSD : 0);
-    if (r > 0) __syncthreads();  // the previous round's tables are no longer read
-    if (use_sk) stage_table<DP>(tsk, p.sk[r] + tb, p.M, p.D);
-    if (dkk_r) stage_table<DP>(tdk, dkk_r + tb, p.M, p.D);
-    if (dkv_r) stage_table<DP>(tdv, dkv_r + tb, p.M, p.D);
-    __syncthreads();
+    float* tdk = seq ? t0 : tsk + (use_sk ? p.M * RSD : 0);
+    float* tdv = seq ? t0 : tdk + (dkk_r ? p.M * RSD : 0);
+    if (!seq) {
+      if (r > 0) __syncthreads();  // the previous round's tables are no longer read
+      if (use_sk) stage_table<DP>(tsk, p.sk[r] + tb, p.M, p.D);
+      if (dkk_r) stage_table<DP>(tdk, dkk_r + tb, p.M, p.D);
+      if (dkv_r) stage_table<DP>(tdv, dkv_r + tb, p.M, p.D);
+      __syncthreads();
+    }
     // the round's passes, specialised on which tables it has
     auto passes = [&](auto sk_c, auto dk_c, auto dv_c) {
       constexpr bool SK = decltype(sk_c)::value, DK = decltype(dk_c)::value, DV = decltype(dv_c)::value;
@@ -411,6 +415,29 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_grad_lds_kernel(TokGradParam
     };
     using Y = std::true_type;
     using N_ = std::false_type;
+    if constexpr (SEQ) {  // each present table: stage it, then its term's passes
+      if (use_sk) {
+        __syncthreads();
+        stage_table<DP>(t0, p.sk[r] + tb, p.M, p.D);
+        __syncthreads();
+        passes(Y{}, N_{}, N_{});
+      }
+      if (dkk_r) {
+        __syncthreads();
+        stage_table<DP>(t0, dkk_r + tb, p.M, p.D);
+        __syncthreads();
+        passes(N_{}, Y{}, N_{});
+      }
+      if constexpr (KV) {
+        if (dkv_r) {
+          __syncthreads();
+          stage_table<DP>(t0, dkv_r + tb, p.M, p.D);
+          __syncthreads();
+          passes(N_{}, N_{}, Y{});
+        }
+      }
+      continue;
+    }
     if constexpr (KV) {
       if (dkv_r) {
         if (use_sk) { if (dkk_r) passes(Y{}, Y{}, Y{}); else passes(Y{}, N_{}, Y{}); }
@@ -533,18 +560,25 @@ hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <typename T, int DP, int PASSES, bool KV, bool WIDE>
-hipError_t launch_tok_grad_lds_w(const TokGradParams& p, int nt, hipStream_t st) {
+template <typename T, int DP, int PASSES, bool KV, bool WIDE, bool SEQ>
+hipError_t launch_tok_grad_lds_s(const TokGradParams& p, int nt, hipStream_t st) {
   using S = TokShape<DP>;
   const int BH = p.B * p.H;
   const int nchunk = (p.N + PASSES * S::TPP - 1) / (PASSES * S::TPP);
-  const size_t lds = (size_t)nt * p.M * S::RSD * 4;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&tok_grad_lds_kernel<T, DP, PASSES, KV, WIDE>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  const size_t lds = (size_t)(SEQ ? 1 : nt) * p.M * S::RSD * 4;
+  const void* fn = reinterpret_cast<const void*>(&tok_grad_lds_kernel<T, DP, PASSES, KV, WIDE, SEQ>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
-  hipLaunchKernelGGL((tok_grad_lds_kernel<T, DP, PASSES, KV, WIDE>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
+  hipLaunchKernelGGL((tok_grad_lds_kernel<T, DP, PASSES, KV, WIDE, SEQ>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
   return hipGetLastError();
+}
+
+template <typename T, int DP, int PASSES, bool KV, bool WIDE>
+hipError_t launch_tok_grad_lds_w(const TokGradParams& p, int nt, hipStream_t st) {
+  // tables that do not fit together are staged one at a time
+  if (tables_fit(nt, p.M, DP)) return launch_tok_grad_lds_s<T, DP, PASSES, KV, WIDE, false>(p, nt, st);
+  return launch_tok_grad_lds_s<T, DP, PASSES, KV, WIDE, true>(p, nt, st);
 }
 
 template <typename T, int DP, int PASSES, bool KV>
@@ -560,7 +594,7 @@ hipError_t launch_tok_grad_t(const TokGradParams& p, hipStream_t st) {
     const int k = ((p.ds[r] && p.dq.p) ? 1 : 0) + (p.dkk[r] ? 1 : 0) + (p.dkv[r] ? 1 : 0);
     nt = k > nt ? k : nt;
   }
-  if (nt > 0 && tables_fit(nt, p.M, DP)) {
+  if (nt > 0 && tables_fit(1, p.M, DP)) {
     // registers: dq only (the slot-key gradient terms go to dq) keeps 8 passes
     // of tokens, with separate token-key / token-value gradients 4
     if (p.shared_kv) return launch_tok_grad_lds<T, DP, 8, false>(p, nt, st);
