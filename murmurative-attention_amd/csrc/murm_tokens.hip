@@ -172,7 +172,7 @@ struct TokShape {
   static constexpr int RSD = table_stride<DP>();       // staged row stride
 };
 
-template <typename T, int DP, int NP, bool HV, bool WIDE>
+template <typename T, int DP, int NP, bool HV, bool WIDE, bool SEQ>
 __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams p, int nchunk) {
   using S = TokShape<DP>;
   constexpr int DCH = S::DCH, TPP = S::TPP, RSD = S::RSD;
@@ -212,35 +212,28 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
   float* tsv = reinterpret_cast<float*>(smem);
   float* tdk = tsv + (has_g ? p.M * RSD : 0);
   float* tdv = tdk + (has_k ? p.M * RSD : 0);
-  float* tdw = tdv + (HV ? p.M * RSD : 0);
+  float* tdw = SEQ ? tsv + p.M * RSD : tdv + (HV ? p.M * RSD : 0);
   const int64_t tb = (int64_t)bh * p.M * p.D;
-  if (has_g) stage_table<DP>(tsv, p.sv + tb, p.M, p.D);
-  if (has_k) stage_table<DP>(tdk, p.dkk + tb, p.M, p.D);
-  if constexpr (HV) stage_table<DP>(tdv, p.dkv + tb, p.M, p.D);
-  if (p.dW)
-    for (int i = threadIdx.x; i < p.M; i += blockDim.x) tdw[i] = p.dW[(int64_t)bh * p.M + i];
-  __syncthreads();
-  // the passes, specialised on which tables are present
-  auto passes = [&](auto g_c, auto k_c) {
-  constexpr bool HG = decltype(g_c)::value, HK = decltype(k_c)::value;
-#pragma unroll
-  for (int q = 0; q < NP; ++q) {
-    const int n = c_beg + q * TPP + threadIdx.x / DCH;
+  auto slots = [&](int q, uint32_t (&sl)[KN]) {
     const uint4 ir = ix[q];
-    const uint32_t sl[KN] = {ir.x & 0xFFFF, ir.x >> 16, ir.y & 0xFFFF, ir.y >> 16,
-                             ir.z & 0xFFFF, ir.z >> 16, ir.w & 0xFFFF};
+    sl[0] = ir.x & 0xFFFF; sl[1] = ir.x >> 16; sl[2] = ir.y & 0xFFFF; sl[3] = ir.y >> 16;
+    sl[4] = ir.z & 0xFFFF; sl[5] = ir.z >> 16; sl[6] = ir.w & 0xFFFF;
+  };
+  // dw_j of pass q from the tables flagged (sums over the token's lanes)
+  auto dots = [&](int q, const uint32_t (&sl)[KN], float (&dw)[KN], const float* ts, const float* tk,
+                  const float* tv, auto g_c, auto k_c, auto v_c) {
+    constexpr bool HG = decltype(g_c)::value, HK = decltype(k_c)::value, HVV = decltype(v_c)::value;
     float g[8], a[8], c[8];
     if constexpr (HG) unraw8s<T, DP>(rg[q], g, dc, sw, p.D);
     if constexpr (HK) unraw8s<T, DP>(rk[q], a, dc, sw, p.D);
-    if constexpr (HV) unraw8s<T, DP>(rv[q], c, dc, sw, p.D);
-    float dw[KN];
+    if constexpr (HVV) unraw8s<T, DP>(rv[q], c, dc, sw, p.D);
     // rows of slot j + 1 are read while slot j's are used; the scheduling
     // barrier keeps the compiler from reading further ahead
     float vs[2][8], vk[2][8], vv[2][8];
     auto rows = [&](int j, int o) {
-      if constexpr (HG) lds8s<DP>(tsv + sl[j] * RSD, dc, sw, vs[o]);
-      if constexpr (HK) lds8s<DP>(tdk + sl[j] * RSD, dc, sw, vk[o]);
-      if constexpr (HV) lds8s<DP>(tdv + sl[j] * RSD, dc, sw, vv[o]);
+      if constexpr (HG) lds8s<DP>(ts + sl[j] * RSD, dc, sw, vs[o]);
+      if constexpr (HK) lds8s<DP>(tk + sl[j] * RSD, dc, sw, vk[o]);
+      if constexpr (HVV) lds8s<DP>(tv + sl[j] * RSD, dc, sw, vv[o]);
     };
     rows(0, 0);
 #pragma unroll
@@ -256,14 +249,17 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
 #pragma unroll
         for (int i = 0; i < 8; ++i) sacc += a[i] * vk[o][i];
       }
-      if constexpr (HV) {
+      if constexpr (HVV) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) sacc += c[i] * vv[o][i];
       }
       dw[j] = group_sum<DCH>(sacc);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // lane dc finishes weights j = dc, dc + DCH, ...
+  };
+  // lane dc finishes weights j = dc, dc + DCH, ... of pass q
+  auto finish = [&](int q, const uint32_t (&sl)[KN], const float (&dw)[KN]) {
+    const int n = c_beg + q * TPP + threadIdx.x / DCH;
     float mine[JPL];
     float part = 0.f;
 #pragma unroll
@@ -290,12 +286,76 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
       if (p.dw_out) p.dw_out[row * KN + jj] = mine[u];
       if (p.ds_out) p.ds_out[row * KN + jj] = wq[q][u] * (mine[u] - dot);
     }
-  }
   };
   using Y = std::true_type;
   using N_ = std::false_type;
-  if (has_g) { if (has_k) passes(Y{}, Y{}); else passes(Y{}, N_{}); }
-  else { if (has_k) passes(N_{}, Y{}); else passes(N_{}, N_{}); }
+  if constexpr (!SEQ) {
+    if (has_g) stage_table<DP>(tsv, p.sv + tb, p.M, p.D);
+    if (has_k) stage_table<DP>(tdk, p.dkk + tb, p.M, p.D);
+    if constexpr (HV) stage_table<DP>(tdv, p.dkv + tb, p.M, p.D);
+    if (p.dW)
+      for (int i = threadIdx.x; i < p.M; i += blockDim.x) tdw[i] = p.dW[(int64_t)bh * p.M + i];
+    __syncthreads();
+    // the passes, specialised on which tables are present
+    auto passes = [&](auto g_c, auto k_c) {
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        uint32_t sl[KN];
+        slots(q, sl);
+        float dw[KN];
+        dots(q, sl, dw, tsv, tdk, tdv, g_c, k_c, std::integral_constant<bool, HV>{});
+        finish(q, sl, dw);
+      }
+    };
+    if (has_g) { if (has_k) passes(Y{}, Y{}); else passes(Y{}, N_{}); }
+    else { if (has_k) passes(N_{}, Y{}); else passes(N_{}, N_{}); }
+  } else {
+    // the tables do not fit together: one at a time in one LDS table, each
+    // table's dot products added to dw per pass, then the weights finished
+    float* t0 = tsv;
+    if (p.dW)  // after the one table
+      for (int i = threadIdx.x; i < p.M; i += blockDim.x) tdw[i] = p.dW[(int64_t)bh * p.M + i];
+    float dwp[NP][KN];
+#pragma unroll
+    for (int q = 0; q < NP; ++q)
+#pragma unroll
+      for (int j = 0; j < KN; ++j) dwp[q][j] = 0.f;
+    auto pass_all = [&](auto g_c, auto k_c, auto v_c) {
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        uint32_t sl[KN];
+        slots(q, sl);
+        float dw[KN];
+        dots(q, sl, dw, t0, t0, t0, g_c, k_c, v_c);
+#pragma unroll
+        for (int j = 0; j < KN; ++j) dwp[q][j] += dw[j];
+      }
+    };
+    if (has_g) {
+      stage_table<DP>(t0, p.sv + tb, p.M, p.D);
+      __syncthreads();
+      pass_all(Y{}, N_{}, N_{});
+      __syncthreads();
+    }
+    if (has_k) {
+      stage_table<DP>(t0, p.dkk + tb, p.M, p.D);
+      __syncthreads();
+      pass_all(N_{}, Y{}, N_{});
+      __syncthreads();
+    }
+    if constexpr (HV) {
+      stage_table<DP>(t0, p.dkv + tb, p.M, p.D);
+      __syncthreads();
+      pass_all(N_{}, N_{}, Y{});
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      uint32_t sl[KN];
+      slots(q, sl);
+      finish(q, sl, dwp[q]);
+    }
+  }
 }
 
 // tok_grad with each round's tables staged in LDS in turn; a thread keeps the
@@ -524,18 +584,25 @@ inline bool wide_rows(std::initializer_list<const TokView*> views, int D) {
   return true;
 }
 
-template <typename T, int DP, int NP, bool HV, bool WIDE>
-hipError_t launch_tok_bwd_lds_w(const TokBwdParams& p, int nt, hipStream_t st) {
+template <typename T, int DP, int NP, bool HV, bool WIDE, bool SEQ>
+hipError_t launch_tok_bwd_lds_s(const TokBwdParams& p, int nt, hipStream_t st) {
   using S = TokShape<DP>;
   const int BH = p.B * p.H;
   const int nchunk = (p.N + NP * S::TPP - 1) / (NP * S::TPP);
-  const size_t lds = (size_t)nt * p.M * S::RSD * 4 + (size_t)p.M * 4;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&tok_bwd_lds_kernel<T, DP, NP, HV, WIDE>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  const size_t lds = (size_t)(SEQ ? 1 : nt) * p.M * S::RSD * 4 + (size_t)p.M * 4;
+  const void* fn = reinterpret_cast<const void*>(&tok_bwd_lds_kernel<T, DP, NP, HV, WIDE, SEQ>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
-  hipLaunchKernelGGL((tok_bwd_lds_kernel<T, DP, NP, HV, WIDE>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
+  hipLaunchKernelGGL((tok_bwd_lds_kernel<T, DP, NP, HV, WIDE, SEQ>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
   return hipGetLastError();
+}
+
+template <typename T, int DP, int NP, bool HV, bool WIDE>
+hipError_t launch_tok_bwd_lds_w(const TokBwdParams& p, int nt, hipStream_t st) {
+  // tables that do not fit together are staged one at a time
+  if (tables_fit(nt, p.M, DP)) return launch_tok_bwd_lds_s<T, DP, NP, HV, WIDE, false>(p, nt, st);
+  return launch_tok_bwd_lds_s<T, DP, NP, HV, WIDE, true>(p, nt, st);
 }
 
 template <typename T, int DP, int NP, bool HV>
@@ -547,7 +614,7 @@ hipError_t launch_tok_bwd_lds(const TokBwdParams& p, int nt, hipStream_t st) {
 template <typename T, int DP>
 hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
   const int nt = (p.sv ? 1 : 0) + (p.dkk ? 1 : 0) + (p.dkv ? 1 : 0);
-  if (nt > 0 && tables_fit(nt, p.M, DP)) {
+  if (nt > 0 && tables_fit(1, p.M, DP)) {
     // tokens per lane whose loads are all in flight at once: 8 (16-bit tokens,
     // two token rows) or 4 (float32 tokens or three token rows)
     if (p.dkv) return launch_tok_bwd_lds<T, DP, 4, true>(p, nt, st);
