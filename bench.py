@@ -8,17 +8,20 @@ README MurmurativeAttention layer's training step.
 A step is one forward+backward of the README-form slot_murmurate over one
 synthetic batch (seeded N(0,1) draws), inputs resident
 in HBM.  `value` is tokens/s over exactly K timed steps (HIP-synchronised on
-both sides).  A second pass over the same K steps records HIP events around
-every kernel launch (on the stream the kernels run on) for the per-kernel
-durations behind the roofline fraction.  The CPU baseline times the CPU oracle
-(a PyTorch restatement of the reference's reference.py) on the host cores.
-Prints one JSON line.
+both sides).  A second pass over the same K steps has every kernel launch
+record start/stop HIP events from its own dispatch (hipExtLaunchKernel, on
+the stream the kernels run on) for the per-kernel durations behind the
+roofline fraction.  The CPU baseline times the CPU oracle (a PyTorch
+restatement of the reference's reference.py) on the host's CPU share.
+`measured_peaks` puts a streaming copy's GB/s and a large bf16 GEMM's TFLOP/s
+beside the spec peaks.  Prints one JSON line.
 """
 
 import argparse
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 
@@ -93,17 +96,27 @@ def call_bytes(B, H, N, D, M, R, e):
     return fwd + bwd
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "slot_murmurate_fwd_bwd_headline_hbm_traffic.md")
+TRAFFIC_FILES = {
+    "3": "slot_murmurate_fwd_bwd_headline_hbm_traffic.md",
+    "4": "slot_murmurate_fwd_bwd_config4_hbm_traffic.md",
+    "5": "murmurative_attention_layer_config5_hbm_traffic.md",
+}
+
+
+def traffic_file(config):
+    name = TRAFFIC_FILES.get(config)
+    return os.path.join(ROOT, "profiles", name) if name else None
 
 
 def measured_traffic(config):
     """HBM bytes per launch of each timing class, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary of the headline run (copy-kernel calibrated);
-    {} for other configs or when the summary is absent."""
-    if config != "3" or not os.path.exists(TRAFFIC_FILE):
+    FETCH_SIZE / WRITE_SIZE summary of this configuration (copy-kernel
+    calibrated); {} when there is none."""
+    path = traffic_file(config)
+    if not path or not os.path.exists(path):
         return {}
     out = {}
-    for line in open(TRAFFIC_FILE):
+    for line in open(path):
         if line.startswith("traffic: "):
             _, cls, val = line.split()
             out[cls] = int(val)
@@ -174,11 +187,44 @@ def module_step(torch, model, opt, x, target):
     return loss
 
 
+def host_cpu():
+    """The host cores the CPU baseline may use and how they were counted.
+
+    threads = the process's CPU share: the cgroup quota when one is set, else
+    the CPUs in its affinity mask, capped by OMP_NUM_THREADS when that is set
+    (one GPU's share of the box's host cores)."""
+    info = {"os_cpu_count": os.cpu_count()}
+    try:
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        info["affinity_cpus"] = os.cpu_count()
+    share = info["affinity_cpus"] or 1
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            info["cgroup_cpu_quota"] = round(int(quota) / int(period), 2)
+            share = min(share, max(1, int(int(quota) / int(period))))
+    except (OSError, ValueError):
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit():
+        info["OMP_NUM_THREADS"] = int(omp)
+        share = min(share, int(omp))
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                info["model"] = line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return share, info
+
+
 def cpu_baseline_module(mc, budget_s=20.0):
     """Time the same training step on the host with the CPU oracle in place of
     the kernels: batch 1, the sequence length cut to fit the time budget."""
     import torch
-    threads = min(16, os.cpu_count() or 1)
+    threads, host = host_cpu()
     torch.set_num_threads(threads)
     cpu = torch.device("cpu")
 
@@ -195,7 +241,8 @@ def cpu_baseline_module(mc, budget_s=20.0):
         n *= 2
     times = sorted(run(n) for _ in range(3))
     med = times[1]
-    return {"value": round(n / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(n / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "host": host,
             "sample": (f"README layer training step (MSE, AdamW) with oracle/murm_oracle.py murmurate_readme "
                        f"in place of the kernels, {mc['dtype']}, B=1, N={n}, dim={mc['dim']}, heads={mc['heads']}, "
                        f"slots={mc['slots']}, R={mc['rounds']}; median of 3, {med:.3f} s; tokens/s = N / time")}
@@ -218,7 +265,7 @@ def cpu_baseline(cfg, budget_s=20.0):
     import torch
     from oracle import murm_oracle as O
     B, H, N, D, M, R, causal, dt, _, _ = cfg
-    threads = min(16, os.cpu_count() or 1)
+    threads, host = host_cpu()
     torch.set_num_threads(threads)
     q, sk, sv, go = make_inputs(cfg, "cpu", seed=42)
 
@@ -236,10 +283,49 @@ def cpu_baseline(cfg, budget_s=20.0):
     med = times[1]
     # heads are independent: the full call costs H/heads times the sample
     tok_s = B * N * heads / (H * med)
-    return {"value": round(tok_s, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(tok_s, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "host": host,
             "sample": (f"oracle/murm_oracle.py murmurate_readme fwd+bwd (autograd), {dt} inputs, "
                        f"B={B}, {heads} of {H} heads, N={N}, d={D}, M={M}, R={R}; median of 3 after "
                        f"1 warm-up, {med:.3f} s; tokens/s = B*N*(heads/H) / time")}
+
+
+def measured_peaks(torch, dev):
+    """Achievable HBM bandwidth and dense bf16 matrix rate on this GPU, beside
+    the spec peaks: a 1 GiB device-to-device copy (torch copy kernel; bytes
+    read + written) and an 8192^3 bf16 GEMM (torch.matmul -> hipBLASLt)."""
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    n = (1 << 30) // 4
+    src = torch.ones(n, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    e0, e1 = ev(), ev()
+    e0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 10 * 2 * n * 4 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, dst
+    K = 8192
+    x = torch.randn(K, K, device=dev, dtype=torch.bfloat16)
+    y = torch.randn(K, K, device=dev, dtype=torch.bfloat16)
+    for _ in range(3):
+        z = torch.matmul(x, y)
+    e0, e1 = ev(), ev()
+    e0.record()
+    for _ in range(10):
+        z = torch.matmul(x, y)
+    e1.record()
+    torch.cuda.synchronize()
+    gemm_tf = 10 * 2 * K ** 3 / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    del x, y, z
+    return {"copy_GB_s": round(copy_gbs, 1), "hbm_spec_GB_s": HBM_PEAK_GBS,
+            "copy_frac_of_spec": round(copy_gbs / HBM_PEAK_GBS, 4),
+            "bf16_gemm_TFLOP_s": round(gemm_tf, 1), "bf16_dense_spec_TFLOP_s": MFMA_BF16_PEAK_TFLOPS,
+            "gemm_frac_of_spec": round(gemm_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "how": "1 GiB float32 copy_ x10 (read + write bytes); 8192^3 bf16 torch.matmul x10; HIP events"}
 
 
 def main():
@@ -320,14 +406,17 @@ def main():
     traffic = measured_traffic(a.config)
     roofline = {"kernel": dom, "bound": "hbm", "achieved": dk["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dk["GB_s"] / HBM_PEAK_GBS, 4), "traffic": traffic.get(dom),
-                "bytes_per_launch": int(per_launch[dom]), "avg_us": dk["avg_us"]}
+                "bytes_per_launch": int(per_launch[dom]), "avg_us": dk["avg_us"],
+                "timing": (f"HIP start/stop events recorded by every launch's own dispatch "
+                           f"(hipExtLaunchKernel) on the kernels' stream, over {a.steps} steps")}
     if traffic.get(dom) is not None:
-        roofline["traffic_source"] = os.path.relpath(TRAFFIC_FILE, ROOT)
+        roofline["traffic_source"] = os.path.relpath(traffic_file(a.config), ROOT)
     if "select_attend" in kt:
-        sa_ms, sa_n = kt["select_attend"]
-        tf = flops["select_attend"] / (sa_ms / sa_n * 1e-3) / 1e12
+        # algorithmic score-GEMM FLOPs over the launch time (the MFMA busy
+        # fraction from hardware counters is in profiles/)
+        tf = flops["select_attend"] / (kernels["select_attend"]["avg_us"] * 1e-6) / 1e12
         kernels["select_attend"]["score_gemm_TFLOPs"] = round(tf, 2)
-        kernels["select_attend"]["mfma_frac"] = round(tf / MFMA_BF16_PEAK_TFLOPS, 4)
+        kernels["select_attend"]["score_gemm_frac_of_bf16_peak"] = round(tf / MFMA_BF16_PEAK_TFLOPS, 4)
     device_ms = sum(ms for ms, _ in kt.values()) / a.steps
     # the whole call against the HBM floor of its algorithmic bytes (slot_murmurate only)
     cb = call_bytes(B, H, N, D, M, R, e)
@@ -361,6 +450,7 @@ def main():
         "kernels": kernels,
         "device_ms_per_step_in_kernels": round(device_ms, 4),
     }
+    res["measured_peaks"] = measured_peaks(torch, dev)
     if a.copy_calibration > 0:
         n = a.copy_calibration * (1 << 20) // 4
         src = torch.ones(n, device=dev)

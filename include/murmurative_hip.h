@@ -15,6 +15,11 @@
  *   indices         int64 [B,H,N,7], weights float32 [B,H,N,7], contiguous.
  *   dtype codes     MURM_F32, MURM_F16, MURM_BF16.
  * Limits: 7 <= M <= 65535, 1 <= D <= 128, rounds <= 16, slots per token = 7.
+ * The entry points that select (murm_select_attend_fwd, murm_select_fwd,
+ * murm_murmurate_fwd) also stage one head's slot keys in the 160 KiB LDS of
+ * a CU, which bounds M by dtype and D: murm_select_max_m() returns the bound
+ * (16-bit tokens: 1024 / 560 / 288 for D <= 32 / 64 / 128; float32 tokens:
+ * 1136 / 592 / 304); larger M returns MURM_ERR_UNSUPPORTED before any launch.
  *
  * Return value: MURM_OK, or an error code with a message readable through
  * murm_last_error() (per thread).  Argument errors are detected on the host
@@ -69,6 +74,11 @@ int murm_select_attend_fwd(int dtype, int slot_dtype, int B, int H, int N, int D
                            void* out, int64_t out_sb, int64_t out_sh, int64_t out_sn,
                            float* weights, int64_t* indices,
                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Largest M the selecting entry points accept for this token dtype and head
+ * dim (0 for an invalid dtype or D).  No counterpart in the reference, whose
+ * CUDA path stops at M*D*2 <= 48 KiB (slot_select_attend.cu:486-490). */
+int murm_select_max_m(int dtype, int D);
 
 /* ---------------------------------------------------------------------------
  * Selection only: int64 indices [B,H,N,7] of the top-7 masked scores, sorted
@@ -251,9 +261,10 @@ int murm_murmurate_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
 
 /* ---------------------------------------------------------------------------
  * Measurement hooks (no counterpart in the reference).  When enabled, every
- * kernel launch is bracketed by HIP events on its stream; murm_timing_read
- * waits for the recorded events and returns the summed device time (ms) and
- * launch count of one kernel class.  Classes: 0 select_attend, 1 gather_out,
+ * kernel launch records a start and a stop HIP event from its own dispatch
+ * (hipExtLaunchKernel), so each pair times the kernel's execution alone;
+ * murm_timing_read waits for the recorded events and returns the summed
+ * device time (ms) and launch count of one kernel class.  Classes: 0 select_attend, 1 gather_out,
  * 2 seg_update, 3 seg_attbwd, 4 du, 5 tok_bwd, 6 tok_grad, 7 conversions,
  * 8 seg_update_reduce, 9 seg_attbwd_reduce (2 and 3 are the partial-sum
  * kernels when 8 and 9 run, else the whole reduction).
@@ -272,6 +283,8 @@ const char* murm_timing_name(int cls);
  * the D layout, to `out` (device, 768 floats).  No counterpart in the
  * reference. */
 int murm_selftest_mfma(float* out, void* stream);
+
+
 
 #ifdef __cplusplus
 }

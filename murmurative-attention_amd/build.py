@@ -28,8 +28,21 @@ INCLUDE = os.path.join(ROOT, "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["murm_select_attend.hip", "murm_slots.hip", "murm_tokens.hip", "murm_capi.hip"]
 EXT_SOURCES = ["torch_binding.cpp", "wrappers.cpp"]
+
+
+def hip_units():
+    """(source, object name, extra flags) of every HIP translation unit: each
+    csrc/*.hip once, except murm_tokens.hip, built once per token dtype."""
+    units = []
+    for src in sorted(f for f in os.listdir(CSRC) if f.endswith(".hip")):
+        stem = src[:-4]
+        if src == "murm_tokens.hip":
+            for dt, sfx in ((0, "f32"), (1, "f16"), (2, "bf16")):
+                units.append((src, f"{stem}_{sfx}.o", [f"-DMURM_TOKENS_DT={dt}"]))
+        else:
+            units.append((src, stem + ".o", []))
+    return units
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
@@ -66,29 +79,53 @@ def _torch_flags():
     return cflags, ldflags
 
 
-def build(jobs: int = 8, verbose: bool = False):
+def _stale(obj, deps):
+    """True when obj is missing or older than any of its dependencies."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def build(jobs: int = 8, verbose: bool = False, incremental: bool = False):
+    """Compile everything (incremental=True skips objects newer than their
+    source and every header they may include)."""
     os.makedirs(BUILD, exist_ok=True)
-    hip_objs = [os.path.join(BUILD, s.replace(".hip", ".o")) for s in HIP_SOURCES]
+    headers = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    headers += [os.path.join(INCLUDE, f) for f in os.listdir(INCLUDE) if f.endswith(".h")]
+    units = hip_units()
+    hip_objs = [os.path.join(BUILD, o) for _, o, _ in units]
     cflags, ldflags = _torch_flags()
     ext_objs = [os.path.join(BUILD, s.replace(".cpp", ".o")) for s in EXT_SOURCES]
+    ext_hdrs = headers + [os.path.join(TEXT, f) for f in os.listdir(TEXT) if f.endswith(".h")]
 
     def hip_job(i):
-        return _run(["hipcc", *HIPCC_FLAGS, "-c", os.path.join(CSRC, HIP_SOURCES[i]), "-o", hip_objs[i]])
+        src, _, extra = units[i]
+        if incremental and not _stale(hip_objs[i], [os.path.join(CSRC, src)] + headers):
+            return ""
+        return _run(["hipcc", *HIPCC_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", hip_objs[i]])
 
     def ext_job(i):
-        return _run(["g++", *cflags, "-c", os.path.join(TEXT, EXT_SOURCES[i]), "-o", ext_objs[i]])
+        src = os.path.join(TEXT, EXT_SOURCES[i])
+        if incremental and not _stale(ext_objs[i], [src] + ext_hdrs):
+            return ""
+        return _run(["g++", *cflags, "-c", src, "-o", ext_objs[i]])
 
+    # the slowest units first, so they start while the rest are queued
+    order = sorted(range(len(units)), key=lambda i: units[i][0] != "murm_tokens.hip")
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        futs = [ex.submit(hip_job, i) for i in range(len(HIP_SOURCES))]
+        futs = [ex.submit(hip_job, i) for i in order]
         futs += [ex.submit(ext_job, i) for i in range(len(EXT_SOURCES))]
         logs = [f.result() for f in futs]
     lib = os.path.join(PKG, "libmurmurative_hip.so")
-    _run(["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libmurmurative_hip.so",
-          *hip_objs, "-o", lib + ".tmp"])
-    os.replace(lib + ".tmp", lib)
+    if not incremental or _stale(lib, hip_objs):
+        _run(["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libmurmurative_hip.so",
+              *hip_objs, "-o", lib + ".tmp"])
+        os.replace(lib + ".tmp", lib)
     ext = os.path.join(PKG, "murmurative_attention_ops.so")
-    _run(["g++", "-shared", *ext_objs, "-o", ext + ".tmp", *ldflags])
-    os.replace(ext + ".tmp", ext)
+    if not incremental or _stale(ext, ext_objs + [lib]):
+        _run(["g++", "-shared", *ext_objs, "-o", ext + ".tmp", *ldflags])
+        os.replace(ext + ".tmp", ext)
     if verbose:
         for l in logs:
             if l.strip():
@@ -100,8 +137,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("-i", "--incremental", action="store_true",
+                    help="skip objects newer than their sources and headers")
     a = ap.parse_args()
-    lib, ext = build(a.jobs, a.verbose)
+    lib, ext = build(a.jobs, a.verbose, a.incremental)
     print("built", os.path.relpath(lib, ROOT), os.path.relpath(ext, ROOT))
 
 

@@ -58,8 +58,14 @@ Timing& timing() {
   return t;
 }
 
+thread_local LaunchEvents g_launch_events{nullptr, nullptr};
+
+// f() enqueues exactly one kernel; with timing on, that launch records a
+// start and a stop event from its own dispatch (hipExtLaunchKernel), so the
+// elapsed time between them is the kernel's execution alone.
 template <typename F>
 int run(int cls, hipStream_t st, const char* what, F&& f) {
+  (void)st;
   Timing& T = timing();
   hipEvent_t e0 = nullptr, e1 = nullptr;
   bool on;
@@ -71,12 +77,18 @@ int run(int cls, hipStream_t st, const char* what, F&& f) {
       e1 = T.get();
     }
   }
-  if (on && e0) (void)hipEventRecord(e0, st);
+  const bool timed = on && e0 && e1;
+  if (timed) g_launch_events = {e0, e1};
   const hipError_t err = f();
-  if (on && e1) {
-    (void)hipEventRecord(e1, st);
+  g_launch_events = {nullptr, nullptr};
+  if (timed) {
     std::lock_guard<std::mutex> lk(T.mu);
-    T.rec[cls].push_back({e0, e1});
+    if (err == hipSuccess) {
+      T.rec[cls].push_back({e0, e1});
+    } else {
+      T.pool.push_back(e0);
+      T.pool.push_back(e1);
+    }
   }
   if (err != hipSuccess) return fail(MURM_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
   return MURM_OK;
@@ -272,6 +284,24 @@ SegParams seg_base(int B, int H, int N, int D, int M) {
   return p;
 }
 
+// Largest M whose slot keys the select kernels stage in one CU's LDS.
+int select_max_m(int dtype, int D) {
+  if (!dtype_ok(dtype) || D < 1 || D > 128) return 0;
+  const int DP = pick_dp(D);
+  int M = 65535 & ~15;
+  while (M >= KN && sa_lds_bytes(dtype, DP, M) > 160 * 1024) M -= 16;
+  return M >= KN ? M : 0;
+}
+
+int select_fits(int dtype, int D, int M) {
+  const int mx = select_max_m(dtype, D);
+  if (M > mx)
+    return fail(MURM_ERR_UNSUPPORTED,
+                "slot keys (M=%d, D=%d) exceed the 160 KiB LDS of one CU: the select kernels take M <= %d here",
+                M, D, mx);
+  return MURM_OK;
+}
+
 int stencil_check(int dt, int B, int H, int M, int D) {
   if (!dtype_ok(dt)) return fail(MURM_ERR_ARG, "unknown dtype code");
   if (B < 1 || H < 1 || M < 1 || D < 1) return fail(MURM_ERR_ARG, "B, H, M, D must be >= 1");
@@ -300,6 +330,15 @@ __global__ void selftest_mfma_kernel(float* out) {
 }
 
 }  // namespace
+
+namespace murm {
+LaunchEvents& launch_events() { return g_launch_events; }
+
+int set_error(int code, const char* msg) {
+  g_err = msg;
+  return code;
+}
+}  // namespace murm
 
 extern "C" {
 
@@ -344,7 +383,7 @@ const char* murm_timing_name(int cls) {
 int murm_selftest_mfma(float* out, void* stream) {
   if (!out) return fail(MURM_ERR_ARG, "out is NULL");
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(selftest_mfma_kernel, dim3(1), dim3(64), 0, st, out);
+  MURM_LAUNCH(selftest_mfma_kernel, dim3(1), dim3(64), 0, st, out);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MURM_OK : fail(MURM_ERR_HIP, "selftest: %s", hipGetErrorString(e));
 }
@@ -365,11 +404,10 @@ int murm_select_attend_fwd(int dtype, int slot_dtype, int B, int H, int N, int D
   int rc = check_geom(dtype, slot_dtype, B, H, N, D, M);
   if (rc) return rc;
   if (!q || !sk || !sv || !out || !weights || !indices) return fail(MURM_ERR_ARG, "NULL tensor pointer");
+  if ((rc = select_fits(dtype, D, M))) return rc;
   OpLayout L = op_layout(workspace, B, H, N, D, M, 0);
   if ((rc = need_ws(workspace, workspace_bytes, L.bytes))) return rc;
   const int DP = pick_dp(D);
-  if (sa_lds_bytes(dtype, DP, M) > 160 * 1024)
-    return fail(MURM_ERR_UNSUPPORTED, "slot keys (M=%d, D=%d) exceed the 160 KiB LDS of one CU", M, D);
   hipStream_t st = (hipStream_t)stream;
   {
     const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk};
@@ -390,6 +428,8 @@ int murm_select_attend_fwd(int dtype, int slot_dtype, int B, int H, int N, int D
   return MURM_OK;
 }
 
+int murm_select_max_m(int dtype, int D) { return select_max_m(dtype, D); }
+
 int murm_select_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, int M, const void* q, int64_t q_sb,
                     int64_t q_sh, int64_t q_sn, const void* sk, int64_t sk_sb, int64_t sk_sh, int64_t sk_sm,
                     const uint8_t* mask, int64_t mk_sb, int64_t mk_sh, int64_t mk_sn, int64_t mk_sm,
@@ -398,11 +438,10 @@ int murm_select_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, int M
   int rc = check_geom(dtype, slot_dtype, B, H, N, D, M);
   if (rc) return rc;
   if (!q || !sk || !indices) return fail(MURM_ERR_ARG, "NULL tensor pointer");
+  if ((rc = select_fits(dtype, D, M))) return rc;
   OpLayout L = op_layout(workspace, B, H, N, D, M, 0);
   if ((rc = need_ws(workspace, workspace_bytes, L.bytes))) return rc;
   const int DP = pick_dp(D);
-  if (sa_lds_bytes(dtype, DP, M) > 160 * 1024)
-    return fail(MURM_ERR_UNSUPPORTED, "slot keys (M=%d, D=%d) exceed the 160 KiB LDS of one CU", M, D);
   hipStream_t st = (hipStream_t)stream;
   RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sk, sk_sb, sk_sh, sk_sm, L.sk, B, H, M, D, st));
   SAParams p = sa_params(B, H, N, D, M, tv_of(q, q_sb, q_sh, q_sn, dtype), L.sk, effective_M, causal, 0.0);
@@ -678,11 +717,10 @@ int murm_murmurate_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
   if (!q || !sk || !sv || !out || !weights_last) return fail(MURM_ERR_ARG, "NULL tensor pointer");
   if ((tk == nullptr) != (tv == nullptr)) return fail(MURM_ERR_ARG, "tk and tv must both be given or both NULL");
   const int shared = tk == nullptr;
+  if ((rc = select_fits(dtype, D, M))) return rc;
   FwdLayout L = fwd_layout(workspace, B, H, N, D, M, rounds, shared);
   if ((rc = need_ws(workspace, workspace_bytes, L.bytes))) return rc;
   const int DP = pick_dp(D);
-  if (sa_lds_bytes(dtype, DP, M) > 160 * 1024)
-    return fail(MURM_ERR_UNSUPPORTED, "slot keys (M=%d, D=%d) exceed the 160 KiB LDS of one CU", M, D);
   hipStream_t st = (hipStream_t)stream;
   const TokView qv = tv_of(q, q_sb, q_sh, q_sn, dtype);
   const TokView kv = shared ? qv : tv_of(tk, tk_sb, tk_sh, tk_sn, dtype);

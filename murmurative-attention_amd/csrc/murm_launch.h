@@ -1,6 +1,7 @@
 // Kernel parameter blocks and launchers (internal to libmurmurative_hip).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -8,6 +9,24 @@
 #include "murm_common.h"
 
 namespace murm {
+
+// Events that the calling thread's next kernel launch records from its own
+// dispatch (start and end of the kernel's execution); null = a plain launch.
+// The C ABI's timing wrapper sets them around exactly one launch.
+struct LaunchEvents {
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+LaunchEvents& launch_events();
+
+#define MURM_LAUNCH(kernel, grid, block, lds, stream, ...)                                           \
+  do {                                                                                               \
+    const ::murm::LaunchEvents _ev = ::murm::launch_events();                                        \
+    if (_ev.start)                                                                                   \
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, _ev.start, _ev.stop, 0, __VA_ARGS__);   \
+    else                                                                                             \
+      hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                             \
+  } while (0)
 
 struct SAParams {
   TokView q;
@@ -115,8 +134,10 @@ struct AttendIdxParams {
   float* w;               // [BH, N, 7]
 };
 
+// Records `msg` as the calling thread's murm_last_error() and returns `code`.
+int set_error(int code, const char* msg);
+
 size_t sa_lds_bytes(int dtype, int DP, int M);
-hipError_t launch_attend_idx(int dtype, int DP, const AttendIdxParams& p, hipStream_t st);
 hipError_t launch_select_attend(int dtype, int DP, const SAParams& p, hipStream_t st);
 hipError_t launch_gather_out(int dtype, int DP, const OutParams& p, hipStream_t st);
 int seg_chunks(int B, int H, int N, int M, int D, int mode);   // 0: shape not served (d > 128)
@@ -127,8 +148,31 @@ bool seg_two_stage(int dtype, int DP, int mode, const SegParams& p, const PartPa
 hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, const PartParams* pp, int stage,
                       hipStream_t st);
 hipError_t launch_du(const DuParams& p, hipStream_t st);
-hipError_t launch_tok_bwd(int dtype, int DP, const TokBwdParams& p, hipStream_t st);
-hipError_t launch_tok_grad(int dtype, int DP, const TokGradParams& p, hipStream_t st);
+// token-side kernels, one translation unit per token dtype (murm_tokens.hip)
+hipError_t launch_tok_bwd_f32(int DP, const TokBwdParams& p, hipStream_t st);
+hipError_t launch_tok_bwd_f16(int DP, const TokBwdParams& p, hipStream_t st);
+hipError_t launch_tok_bwd_bf16(int DP, const TokBwdParams& p, hipStream_t st);
+hipError_t launch_tok_grad_f32(int DP, const TokGradParams& p, hipStream_t st);
+hipError_t launch_tok_grad_f16(int DP, const TokGradParams& p, hipStream_t st);
+hipError_t launch_tok_grad_bf16(int DP, const TokGradParams& p, hipStream_t st);
+hipError_t launch_attend_idx_f32(int DP, const AttendIdxParams& p, hipStream_t st);
+hipError_t launch_attend_idx_f16(int DP, const AttendIdxParams& p, hipStream_t st);
+hipError_t launch_attend_idx_bf16(int DP, const AttendIdxParams& p, hipStream_t st);
+inline hipError_t launch_tok_bwd(int dtype, int DP, const TokBwdParams& p, hipStream_t st) {
+  return dtype == DT_F32 ? launch_tok_bwd_f32(DP, p, st)
+       : dtype == DT_F16 ? launch_tok_bwd_f16(DP, p, st)
+       : dtype == DT_BF16 ? launch_tok_bwd_bf16(DP, p, st) : hipErrorInvalidValue;
+}
+inline hipError_t launch_tok_grad(int dtype, int DP, const TokGradParams& p, hipStream_t st) {
+  return dtype == DT_F32 ? launch_tok_grad_f32(DP, p, st)
+       : dtype == DT_F16 ? launch_tok_grad_f16(DP, p, st)
+       : dtype == DT_BF16 ? launch_tok_grad_bf16(DP, p, st) : hipErrorInvalidValue;
+}
+inline hipError_t launch_attend_idx(int dtype, int DP, const AttendIdxParams& p, hipStream_t st) {
+  return dtype == DT_F32 ? launch_attend_idx_f32(DP, p, st)
+       : dtype == DT_F16 ? launch_attend_idx_f16(DP, p, st)
+       : dtype == DT_BF16 ? launch_attend_idx_bf16(DP, p, st) : hipErrorInvalidValue;
+}
 template <typename S, typename D>
 struct SlotConv {   // one slot tensor [B,H,M,D] (element strides) <-> fp32 state [BH,M,D]
   S src;

@@ -579,9 +579,9 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     if (wide)
-      hipLaunchKernelGGL((sa_kernel16<T, DP, true>), grid, dim3(64 * SA16_WAVES), lds, st, p);
+      MURM_LAUNCH((sa_kernel16<T, DP, true>), grid, dim3(64 * SA16_WAVES), lds, st, p);
     else
-      hipLaunchKernelGGL((sa_kernel16<T, DP, false>), grid, dim3(64 * SA16_WAVES), lds, st, p);
+      MURM_LAUNCH((sa_kernel16<T, DP, false>), grid, dim3(64 * SA16_WAVES), lds, st, p);
   } else {
     dim3 grid((p.N + SAShape<DP>::TOK - 1) / SAShape<DP>::TOK, p.B * p.H);
     const size_t lds = (size_t)Mp * (DP + 4) * sizeof(float);
@@ -589,7 +589,7 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sa_kernel32<DP>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((sa_kernel32<DP>), grid, dim3(256), lds, st, p);
+    MURM_LAUNCH((sa_kernel32<DP>), grid, dim3(256), lds, st, p);
   }
   return hipGetLastError();
 }
@@ -608,14 +608,14 @@ hipError_t launch_out_t(const OutParams& p, hipStream_t st) {
     if (e != hipSuccess) return e;
     dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
     if (wide)
-      hipLaunchKernelGGL((gather_out_lds_kernel<T, DP, true>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
+      MURM_LAUNCH((gather_out_lds_kernel<T, DP, true>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
     else
-      hipLaunchKernelGGL((gather_out_lds_kernel<T, DP, false>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
+      MURM_LAUNCH((gather_out_lds_kernel<T, DP, false>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
     return hipGetLastError();
   }
   constexpr int TPB = 256 / (DP / 8);
   dim3 grid((p.N + TPB - 1) / TPB, p.B * p.H);
-  hipLaunchKernelGGL((gather_out_kernel<T, DP>), grid, dim3(256), 0, st, p);
+  MURM_LAUNCH((gather_out_kernel<T, DP>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 

@@ -1070,9 +1070,10 @@ __global__ void idx_pack_kernel(const int64_t* __restrict__ src, uint16_t* __res
 }
 
 // In-place Jacobi stencil (or its adjoint into `out`) along M; one thread
-// walks one (b,h,d) column keeping the neighbours it has overwritten.
+// walks one (b,h,d) column keeping the neighbours it has overwritten.  The
+// forward passes the same tensor as x and out, so neither is __restrict__.
 template <typename T>
-__global__ void stencil_kernel(T* __restrict__ x, int64_t sb, int64_t sh, int64_t sm, T* __restrict__ out,
+__global__ void stencil_kernel(T* x, int64_t sb, int64_t sh, int64_t sm, T* out,
                                int64_t ob, int64_t oh, int64_t om, int B, int H, int M, int D,
                                float g, int adjoint) {
   const int64_t col = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -1137,10 +1138,10 @@ hipError_t launch_part(const SegParams& p, const PartParams& pp, int nvec, int M
     const int nsg = (p.M + MS - 1) / MS;
     dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk * nsg);
     const int threads = MS * nvec * (DP / 32);
-    hipLaunchKernelGGL((seg_partial_kernel<T, DP, MODE>), grid, dim3(threads), lds, st, p, pp);
+    MURM_LAUNCH((seg_partial_kernel<T, DP, MODE>), grid, dim3(threads), lds, st, p, pp);
   } else {
     const int G = (p.M + GS - 1) / GS;
-    hipLaunchKernelGGL((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G),
+    MURM_LAUNCH((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G),
                        dim3(red_threads(pp.nchunk, DP)), 0,
                        st, p, pp);
   }
@@ -1173,10 +1174,10 @@ hipError_t launch_mma(const SegParams& p, const PartParams& pp, int stage, hipSt
     if (e != hipSuccess) return e;
     const int nsg = (p.M + Sh::MS - 1) / Sh::MS;
     dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk * nsg);
-    hipLaunchKernelGGL((seg_mma_kernel<T, DP, MODE, NV, MSUBT, TG>), grid, dim3(Sh::THREADS), Sh::LDS, st, p, pp);
+    MURM_LAUNCH((seg_mma_kernel<T, DP, MODE, NV, MSUBT, TG>), grid, dim3(Sh::THREADS), Sh::LDS, st, p, pp);
   } else {
     const int G = (p.M + GS - 1) / GS;
-    hipLaunchKernelGGL((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G),
+    MURM_LAUNCH((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G),
                        dim3(red_threads(pp.nchunk, DP)), 0, st, p, pp);
   }
   return hipGetLastError();
@@ -1261,7 +1262,7 @@ hipError_t launch_seg(int dtype, int DP, int mode, const SegParams& p, const Par
 }
 
 hipError_t launch_du(const DuParams& p, hipStream_t st) {
-  hipLaunchKernelGGL(du_kernel, dim3((p.M + 3) / 4, p.B * p.H), dim3(256), 0, st, p);
+  MURM_LAUNCH(du_kernel, dim3((p.M + 3) / 4, p.B * p.H), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -1276,13 +1277,13 @@ hipError_t launch_to_state2(int dtype, const SlotConv<const void*, float*>& a,
   if (total4 < (int64_t(1) << 30)) {  // 32-bit indices, grid-stride step included
     const dim3 g4(grid1d(total4), bp ? 2 : 1);
     switch (dtype) {
-      case DT_BF16: hipLaunchKernelGGL((to_state4_kernel<__bf16>), g4, dim3(256), 0, st,
+      case DT_BF16: MURM_LAUNCH((to_state4_kernel<__bf16>), g4, dim3(256), 0, st,
                                        cv(a, (const __bf16*)nullptr), cv(bb, (const __bf16*)nullptr), H, M, D,
                                        (int)total4); break;
-      case DT_F16: hipLaunchKernelGGL((to_state4_kernel<_Float16>), g4, dim3(256), 0, st,
+      case DT_F16: MURM_LAUNCH((to_state4_kernel<_Float16>), g4, dim3(256), 0, st,
                                       cv(a, (const _Float16*)nullptr), cv(bb, (const _Float16*)nullptr), H, M, D,
                                       (int)total4); break;
-      case DT_F32: hipLaunchKernelGGL((to_state4_kernel<float>), g4, dim3(256), 0, st,
+      case DT_F32: MURM_LAUNCH((to_state4_kernel<float>), g4, dim3(256), 0, st,
                                       cv(a, (const float*)nullptr), cv(bb, (const float*)nullptr), H, M, D,
                                       (int)total4); break;
       default: return hipErrorInvalidValue;
@@ -1291,12 +1292,12 @@ hipError_t launch_to_state2(int dtype, const SlotConv<const void*, float*>& a,
   }
   const dim3 grid(grid1d((int64_t)B * H * M * D), bp ? 2 : 1);
   switch (dtype) {
-    case DT_BF16: hipLaunchKernelGGL((to_state_kernel<__bf16>), grid, dim3(256), 0, st,
+    case DT_BF16: MURM_LAUNCH((to_state_kernel<__bf16>), grid, dim3(256), 0, st,
                                      cv(a, (const __bf16*)nullptr), cv(bb, (const __bf16*)nullptr), B, H, M, D); break;
-    case DT_F16: hipLaunchKernelGGL((to_state_kernel<_Float16>), grid, dim3(256), 0, st,
+    case DT_F16: MURM_LAUNCH((to_state_kernel<_Float16>), grid, dim3(256), 0, st,
                                     cv(a, (const _Float16*)nullptr), cv(bb, (const _Float16*)nullptr), B, H, M, D);
       break;
-    case DT_F32: hipLaunchKernelGGL((to_state_kernel<float>), grid, dim3(256), 0, st,
+    case DT_F32: MURM_LAUNCH((to_state_kernel<float>), grid, dim3(256), 0, st,
                                     cv(a, (const float*)nullptr), cv(bb, (const float*)nullptr), B, H, M, D); break;
     default: return hipErrorInvalidValue;
   }
@@ -1314,12 +1315,12 @@ hipError_t launch_from_state2(int dtype, const SlotConv<const float*, void*>& a,
   if (total4 < (int64_t(1) << 30)) {  // 32-bit indices, grid-stride step included
     const dim3 g4(grid1d(total4), bp ? 2 : 1);
     switch (dtype) {
-      case DT_BF16: hipLaunchKernelGGL((from_state4_kernel<__bf16>), g4, dim3(256), 0, st,
+      case DT_BF16: MURM_LAUNCH((from_state4_kernel<__bf16>), g4, dim3(256), 0, st,
                                        cv(a, (__bf16*)nullptr), cv(bb, (__bf16*)nullptr), H, M, D, (int)total4); break;
-      case DT_F16: hipLaunchKernelGGL((from_state4_kernel<_Float16>), g4, dim3(256), 0, st,
+      case DT_F16: MURM_LAUNCH((from_state4_kernel<_Float16>), g4, dim3(256), 0, st,
                                       cv(a, (_Float16*)nullptr), cv(bb, (_Float16*)nullptr), H, M, D, (int)total4);
         break;
-      case DT_F32: hipLaunchKernelGGL((from_state4_kernel<float>), g4, dim3(256), 0, st,
+      case DT_F32: MURM_LAUNCH((from_state4_kernel<float>), g4, dim3(256), 0, st,
                                       cv(a, (float*)nullptr), cv(bb, (float*)nullptr), H, M, D, (int)total4); break;
       default: return hipErrorInvalidValue;
     }
@@ -1327,11 +1328,11 @@ hipError_t launch_from_state2(int dtype, const SlotConv<const float*, void*>& a,
   }
   const dim3 grid(grid1d((int64_t)B * H * M * D), bp ? 2 : 1);
   switch (dtype) {
-    case DT_BF16: hipLaunchKernelGGL((from_state_kernel<__bf16>), grid, dim3(256), 0, st,
+    case DT_BF16: MURM_LAUNCH((from_state_kernel<__bf16>), grid, dim3(256), 0, st,
                                      cv(a, (__bf16*)nullptr), cv(bb, (__bf16*)nullptr), B, H, M, D); break;
-    case DT_F16: hipLaunchKernelGGL((from_state_kernel<_Float16>), grid, dim3(256), 0, st,
+    case DT_F16: MURM_LAUNCH((from_state_kernel<_Float16>), grid, dim3(256), 0, st,
                                     cv(a, (_Float16*)nullptr), cv(bb, (_Float16*)nullptr), B, H, M, D); break;
-    case DT_F32: hipLaunchKernelGGL((from_state_kernel<float>), grid, dim3(256), 0, st,
+    case DT_F32: MURM_LAUNCH((from_state_kernel<float>), grid, dim3(256), 0, st,
                                     cv(a, (float*)nullptr), cv(bb, (float*)nullptr), B, H, M, D); break;
     default: return hipErrorInvalidValue;
   }
@@ -1349,7 +1350,7 @@ hipError_t launch_from_state(int dtype, const float* src, void* dst, int64_t sb,
 }
 
 hipError_t launch_idx_pack(const int64_t* src, uint16_t* dst, int64_t rows, int K, int M, hipStream_t st) {
-  hipLaunchKernelGGL(idx_pack_kernel, dim3(grid1d(rows)), dim3(256), 0, st, src, dst, rows, K, M);
+  MURM_LAUNCH(idx_pack_kernel, dim3(grid1d(rows)), dim3(256), 0, st, src, dst, rows, K, M);
   return hipGetLastError();
 }
 
@@ -1359,11 +1360,11 @@ hipError_t launch_stencil(int dtype, void* x, int64_t sb, int64_t sh, int64_t sm
   const int64_t cols = (int64_t)B * H * D;
   const int grid = (int)((cols + 255) / 256);
   switch (dtype) {
-    case DT_BF16: hipLaunchKernelGGL((stencil_kernel<__bf16>), dim3(grid), dim3(256), 0, st, (__bf16*)x,
+    case DT_BF16: MURM_LAUNCH((stencil_kernel<__bf16>), dim3(grid), dim3(256), 0, st, (__bf16*)x,
                                      sb, sh, sm, (__bf16*)out, ob, oh, om, B, H, M, D, g, adjoint); break;
-    case DT_F16: hipLaunchKernelGGL((stencil_kernel<_Float16>), dim3(grid), dim3(256), 0, st, (_Float16*)x,
+    case DT_F16: MURM_LAUNCH((stencil_kernel<_Float16>), dim3(grid), dim3(256), 0, st, (_Float16*)x,
                                     sb, sh, sm, (_Float16*)out, ob, oh, om, B, H, M, D, g, adjoint); break;
-    case DT_F32: hipLaunchKernelGGL((stencil_kernel<float>), dim3(grid), dim3(256), 0, st, (float*)x,
+    case DT_F32: MURM_LAUNCH((stencil_kernel<float>), dim3(grid), dim3(256), 0, st, (float*)x,
                                     sb, sh, sm, (float*)out, ob, oh, om, B, H, M, D, g, adjoint); break;
     default: return hipErrorInvalidValue;
   }

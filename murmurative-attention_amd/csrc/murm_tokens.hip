@@ -566,7 +566,7 @@ template <typename T, int DP>
 hipError_t launch_attend_idx_t(const AttendIdxParams& p, hipStream_t st) {
   constexpr int TPB = 256 / (DP / 8);
   dim3 grid((p.N + TPB - 1) / TPB, p.B * p.H);
-  hipLaunchKernelGGL((attend_idx_kernel<T, DP>), grid, dim3(256), 0, st, p);
+  MURM_LAUNCH((attend_idx_kernel<T, DP>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -594,7 +594,7 @@ hipError_t launch_tok_bwd_lds_s(const TokBwdParams& p, int nt, hipStream_t st) {
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
-  hipLaunchKernelGGL((tok_bwd_lds_kernel<T, DP, NP, HV, WIDE, SEQ>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
+  MURM_LAUNCH((tok_bwd_lds_kernel<T, DP, NP, HV, WIDE, SEQ>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
   return hipGetLastError();
 }
 
@@ -623,7 +623,7 @@ hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
   }
   constexpr int TPB = 256 / (DP / 8);
   dim3 grid((p.N + TPB - 1) / TPB, p.B * p.H);
-  hipLaunchKernelGGL((tok_bwd_kernel<T, DP>), grid, dim3(256), 0, st, p);
+  MURM_LAUNCH((tok_bwd_kernel<T, DP>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
@@ -637,7 +637,7 @@ hipError_t launch_tok_grad_lds_s(const TokGradParams& p, int nt, hipStream_t st)
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
-  hipLaunchKernelGGL((tok_grad_lds_kernel<T, DP, PASSES, KV, WIDE, SEQ>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
+  MURM_LAUNCH((tok_grad_lds_kernel<T, DP, PASSES, KV, WIDE, SEQ>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
   return hipGetLastError();
 }
 
@@ -669,61 +669,55 @@ hipError_t launch_tok_grad_t(const TokGradParams& p, hipStream_t st) {
   }
   constexpr int TPB = 256 / (DP / 8);
   dim3 grid((p.N + TPB - 1) / TPB, p.B * p.H);
-  hipLaunchKernelGGL((tok_grad_kernel<T, DP>), grid, dim3(256), 0, st, p);
+  MURM_LAUNCH((tok_grad_kernel<T, DP>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_tok_bwd(int dtype, int DP, const TokBwdParams& p, hipStream_t st) {
-#define MURM_TB(T)                                            \
-  switch (DP) {                                               \
-    case 32: return launch_tok_bwd_t<T, 32>(p, st);           \
-    case 64: return launch_tok_bwd_t<T, 64>(p, st);           \
-    case 128: return launch_tok_bwd_t<T, 128>(p, st);         \
-    default: return hipErrorInvalidValue;                     \
-  }
-  switch (dtype) {
-    case DT_BF16: MURM_TB(__bf16)
-    case DT_F16: MURM_TB(_Float16)
-    case DT_F32: MURM_TB(float)
+// This file is compiled once per token dtype (build.py passes
+// -DMURM_TOKENS_DT=0 float32, 1 float16, 2 bfloat16), so the three sets of
+// kernel instances build in parallel; murm_launch.h dispatches on the dtype.
+#if !defined(MURM_TOKENS_DT)
+#error "build murm_tokens.hip with -DMURM_TOKENS_DT=0 (float32), 1 (float16) or 2 (bfloat16)"
+#elif MURM_TOKENS_DT == 0
+using TokT = float;
+#define MURM_TOK_FN(name) name##_f32
+#elif MURM_TOKENS_DT == 1
+using TokT = _Float16;
+#define MURM_TOK_FN(name) name##_f16
+#elif MURM_TOKENS_DT == 2
+using TokT = __bf16;
+#define MURM_TOK_FN(name) name##_bf16
+#else
+#error "MURM_TOKENS_DT must be 0, 1 or 2"
+#endif
+
+hipError_t MURM_TOK_FN(launch_tok_bwd)(int DP, const TokBwdParams& p, hipStream_t st) {
+  switch (DP) {
+    case 32: return launch_tok_bwd_t<TokT, 32>(p, st);
+    case 64: return launch_tok_bwd_t<TokT, 64>(p, st);
+    case 128: return launch_tok_bwd_t<TokT, 128>(p, st);
     default: return hipErrorInvalidValue;
   }
-#undef MURM_TB
 }
 
-hipError_t launch_attend_idx(int dtype, int DP, const AttendIdxParams& p, hipStream_t st) {
-#define MURM_AI(T)                                            \
-  switch (DP) {                                               \
-    case 32: return launch_attend_idx_t<T, 32>(p, st);        \
-    case 64: return launch_attend_idx_t<T, 64>(p, st);        \
-    case 128: return launch_attend_idx_t<T, 128>(p, st);      \
-    default: return hipErrorInvalidValue;                     \
-  }
-  switch (dtype) {
-    case DT_BF16: MURM_AI(__bf16)
-    case DT_F16: MURM_AI(_Float16)
-    case DT_F32: MURM_AI(float)
+hipError_t MURM_TOK_FN(launch_attend_idx)(int DP, const AttendIdxParams& p, hipStream_t st) {
+  switch (DP) {
+    case 32: return launch_attend_idx_t<TokT, 32>(p, st);
+    case 64: return launch_attend_idx_t<TokT, 64>(p, st);
+    case 128: return launch_attend_idx_t<TokT, 128>(p, st);
     default: return hipErrorInvalidValue;
   }
-#undef MURM_AI
 }
 
-hipError_t launch_tok_grad(int dtype, int DP, const TokGradParams& p, hipStream_t st) {
-#define MURM_TG(T)                                            \
-  switch (DP) {                                               \
-    case 32: return launch_tok_grad_t<T, 32>(p, st);          \
-    case 64: return launch_tok_grad_t<T, 64>(p, st);          \
-    case 128: return launch_tok_grad_t<T, 128>(p, st);        \
-    default: return hipErrorInvalidValue;                     \
-  }
-  switch (dtype) {
-    case DT_BF16: MURM_TG(__bf16)
-    case DT_F16: MURM_TG(_Float16)
-    case DT_F32: MURM_TG(float)
+hipError_t MURM_TOK_FN(launch_tok_grad)(int DP, const TokGradParams& p, hipStream_t st) {
+  switch (DP) {
+    case 32: return launch_tok_grad_t<TokT, 32>(p, st);
+    case 64: return launch_tok_grad_t<TokT, 64>(p, st);
+    case 128: return launch_tok_grad_t<TokT, 128>(p, st);
     default: return hipErrorInvalidValue;
   }
-#undef MURM_TG
 }
 
 }  // namespace murm

@@ -26,6 +26,7 @@ SIGNATURES = {
     "murm_select_attend_workspace_bytes": (_sz, [_i] * 5),
     "murm_select_attend_fwd": (_i, _geom + _view * 3 + _view4 * 2 + [_i, _d, _i] + _view
                                + [_p, _p, _p, _sz, _p]),
+    "murm_select_max_m": (_i, [_i, _i]),
     "murm_select_fwd": (_i, _geom + _view * 2 + _view4 * 2 + [_i, _i, _p, _p, _sz, _p]),
     "murm_attend_fwd": (_i, _geom + _view * 3 + [_p, _d] + _view + [_p, _p, _sz, _p]),
     "murm_select_attend_bwd_workspace_bytes": (_sz, [_i] * 5),

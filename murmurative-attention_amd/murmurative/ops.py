@@ -314,10 +314,14 @@ def _readme_reference(q, slots_k, slots_v, rounds, causal, alpha, gamma):
     return x, idx, w
 
 
-def _slot_murmurate_readme(q, slots_k, slots_v, rounds=3, top_k=K_NEIGHBORS, causal=False, alpha=0.9,
+def _slot_murmurate_readme(q, slots_k, slots_v=None, rounds=3, top_k=K_NEIGHBORS, causal=False, alpha=0.9,
                            gamma=0.15, use_reference=False):
     if top_k != K_NEIGHBORS:
         raise ValueError(f"top_k must be {K_NEIGHBORS} (got {top_k})")
+    if slots_v is None:
+        # README.md:64-67 calls slot_murmurate(x, slots, rounds=3): the slot
+        # values start at zero, as the README layer passes them (README.md:99)
+        slots_v = torch.zeros_like(slots_k)
     if q.dim() != 4 or slots_k.dim() != 4 or slots_v.dim() != 4:
         raise ValueError("q, slots_k and slots_v must be 4-D ([B,H,N,D] and [B,H,M,D])")
     if use_reference:
@@ -380,11 +384,12 @@ def slot_murmurate(*args, **kwargs):
     """Murmurative Attention: R rounds of select -> attend -> update -> diffuse.
 
     README form (q.dim() == 4):
-        slot_murmurate(q, slots_k, slots_v, rounds=3, top_k=7, causal=False,
+        slot_murmurate(q, slots_k, slots_v=None, rounds=3, top_k=7, causal=False,
                        alpha=0.9, gamma=0.15, use_reference=False)
         -> (out [B,H,N,D], indices int64 [B,H,N,7], weights float32 [B,H,N,7])
     with out = q + sum over rounds of the attention output, and indices and
-    weights of the last round.
+    weights of the last round.  slots_v=None starts the slot values at zero
+    (the README's verify call, slot_murmurate(x, slots, rounds=3)).
 
     Projection form (x.dim() == 3, reference ops.py:330-348):
         slot_murmurate(x, q_proj, k_proj, v_proj, slot_k_emb, slot_v_emb,

@@ -83,14 +83,24 @@ def check_selection(name, gpu_idx, scores, k=7):
     return float(set_ok.double().mean())
 
 
-def grad_w_bound(tk, tv, gk, gv, idx, w, alpha, eps=1e-8):
-    """Float32 error bound of the update's weight gradient.
+# Unit roundoff of the slot sums behind the update's weight gradient, per
+# token dtype: float32 tokens sum in float32 (2^-24 per add, 2^-20 covers the
+# sums' length); 16-bit tokens multiply hi + lo halves of the coefficients on
+# MFMA, which represent a float32 coefficient to 2^-17 (bf16) or 2^-22
+# (fp16) relative, on top of the float32 accumulation.  Pinned on the CPU in
+# tests/test_parity_bounds.py.
+U_GRADW = {torch.float32: 2.0 ** -20, torch.float16: 2.0 ** -20, torch.bfloat16: 2.0 ** -17}
+
+
+def grad_w_bound(tk, tv, gk, gv, idx, w, alpha, dtype=torch.bfloat16, eps=1e-8):
+    """Error bound of the update's weight gradient evaluated with the slot
+    sums at the precision of `dtype`'s kernel path (U_GRADW).
 
     dw_nj = (1-a)/(W_m+eps) [(tk_n - K_m/(W_m+eps)).G'k_m + (tv_n - V_m/(W_m+eps)).G'v_m],
     m = idx_nj: the two halves cancel on slots whose total weight W_m is small,
-    so any float32 evaluation (the reference's included) carries an error of
-    about D * 2^-24 * (1-a)/W_m * (|tk|+|mean|).|G'| -- bounded here with
-    2^-17 per term (D <= 128)."""
+    so a relative error u in the sums K, V, W becomes an absolute error of
+    about u * cond with cond = (1-a)/W_m * (|tk|+|mean|).|G'| -- whoever
+    evaluates it (a float32 evaluation of the reference's maths included)."""
     M = gk.shape[2]
     tk, tv, gk, gv = (t.double() for t in (tk, tv, gk, gv))
     K, V, W = O.slot_sums(tk, tv, idx, w.double(), M)
@@ -101,7 +111,7 @@ def grad_w_bound(tk, tv, gk, gv, idx, w, alpha, eps=1e-8):
     ag = lambda t: t.abs()[b, h, idx]  # noqa: E731
     mag = ((tk.abs().unsqueeze(3) + ag(mk)) * ag(gk)).sum(-1) + ((tv.abs().unsqueeze(3) + ag(mv)) * ag(gv)).sum(-1)
     cond = (1.0 - alpha) / (W[b, h, idx] + eps) * mag
-    return cond * 2.0 ** -17
+    return cond * U_GRADW[dtype]
 
 
 def round_indices(ws, B, H, N, D, M, R, shared, r):

@@ -112,3 +112,27 @@ def test_api_value_errors():
     s = torch.randn(1, 2, 16, 8)
     with pytest.raises(ValueError, match="top_k"):
         murmurative.slot_murmurate(q, s, s, rounds=2, top_k=5, use_reference=True)
+
+
+def test_select_lds_bound_without_gpu():
+    # the selecting entry points bound M by the LDS staging of one head's keys
+    lib = capi.load()
+    expect = {(capi.BF16, 32): 1024, (capi.BF16, 64): 560, (capi.BF16, 128): 288,
+              (capi.F16, 64): 560, (capi.F32, 32): 1136, (capi.F32, 64): 592, (capi.F32, 128): 304}
+    for (dt, D), m in expect.items():
+        assert lib.murm_select_max_m(dt, D) == m, (dt, D)
+    assert lib.murm_select_max_m(capi.BF16, 129) == 0 and lib.murm_select_max_m(9, 64) == 0
+    # one slot past the bound is refused on the host, before any launch
+    # (the tensor pointers are never dereferenced on this path)
+    P = ctypes.c_void_p
+    fake = P(4096)
+    for dt, D in ((capi.BF16, 128), (capi.F32, 64)):
+        M = lib.murm_select_max_m(dt, D) + 1
+        rc = lib.murm_select_attend_fwd(dt, dt, 1, 1, 16, D, M, fake, 0, 0, D, fake, 0, 0, D, fake, 0, 0, D,
+                                        None, 0, 0, 0, 0, None, 0, 0, 0, 0, 0, 0.0, 0, fake, 0, 0, D, fake, fake,
+                                        fake, 1 << 40, None)
+        assert rc == capi.ERR_UNSUPPORTED and b"LDS" in lib.murm_last_error(), (dt, D)
+        rc = lib.murm_murmurate_fwd(dt, dt, 1, 1, 16, D, M, 3, 0.9, 0.15, 0, 0, 0.0, fake, 0, 0, D,
+                                    None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, fake, 0, 0, D, fake, 0, 0, D,
+                                    None, 0, 0, 0, 0, fake, 0, 0, D, fake, fake, fake, 1 << 40, None)
+        assert rc == capi.ERR_UNSUPPORTED and b"LDS" in lib.murm_last_error(), (dt, D)

@@ -199,7 +199,7 @@ def test_update_and_diffusion_ops(dtype, case):
     assert_close("update bwd token values", gtv, tv64.grad, dtype)
     assert_close("update bwd slot keys", gok, sk64.grad, dtype)
     assert_close("update bwd slot values", gov, sv64.grad, dtype)
-    assert_close("update bwd weights", gw_, w64.grad, dtype, extra=grad_w_bound(tk, tv, gk, gv, idx, w, a))
+    assert_close("update bwd weights", gw_, w64.grad, dtype, extra=grad_w_bound(tk, tv, gk, gv, idx, w, a, dtype))
     # update + diffusion through autograd: the adjoint crosses the op boundary
     # in the slot dtype (ops.py:188-208), so the oracle rounds it there too
     tkd, tvd, skg, svg = (t.to(DEV).requires_grad_(True) for t in (tk, tv, sk, sv))
@@ -216,7 +216,7 @@ def test_update_and_diffusion_ops(dtype, case):
     assert_close("chain bwd token values", tvd.grad, tv64.grad, dtype)
     assert_close("chain bwd slot keys", skg.grad, sk64.grad, dtype)
     assert_close("chain bwd slot values", svg.grad, sv64.grad, dtype)
-    assert_close("chain bwd weights", wd.grad, w64.grad, dtype, extra=grad_w_bound(tk, tv, gpk, gpv, idx, w, a))
+    assert_close("chain bwd weights", wd.grad, w64.grad, dtype, extra=grad_w_bound(tk, tv, gpk, gpv, idx, w, a, dtype))
     # diffusion backward op alone
     gdk, gdv = lib.slot_diffusion_backward(gk.to(DEV), gv.to(DEV), gm)
     assert_close("diffusion adjoint k", gdk, O.diffusion_transpose(gk.double(), gm), dtype)

@@ -58,3 +58,19 @@ def test_eager_composites_match_oracle():
                                    use_reference=True)
     o2, i2, w2 = O.murmurate_readme(qh, ske.expand(B, -1, -1, -1), sve.expand(B, -1, -1, -1), rounds=3)
     assert torch.allclose(out, o2, atol=1e-5) and torch.equal(idx, i2)
+
+
+def test_readme_verify_call_on_the_eager_path():
+    # README.md:64-67: slot_murmurate(x, slots, rounds=3), slot values zero;
+    # the fixture was written by the reference's own function (config-1 shapes)
+    import os
+    import numpy as np
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "legacy_composite.npz"))
+    B, N, H, Dh, Mm, R = [int(v) for v in d["readme_cfg1__meta"]]
+    x = torch.from_numpy(d["readme_cfg1__q"])
+    slots = torch.from_numpy(d["readme_cfg1__ske"]).unsqueeze(0).expand(B, -1, -1, -1)
+    out, idx, w = M.slot_murmurate(x, slots, rounds=3, use_reference=True)
+    assert out.shape == (B, H, N, Dh) and idx.shape == (B, H, N, 7) and w.shape == (B, H, N, 7)
+    assert torch.allclose(out, torch.from_numpy(d["readme_cfg1__out"]), atol=2e-5, rtol=1e-5)
+    out2, idx2, _ = M.slot_murmurate(x, slots, torch.zeros_like(slots), rounds=3, use_reference=True)
+    assert torch.equal(out, out2) and torch.equal(idx, idx2)
