@@ -284,7 +284,28 @@ const char* murm_timing_name(int cls);
  * reference. */
 int murm_selftest_mfma(float* out, void* stream);
 
-
+/* ---------------------------------------------------------------------------
+ * Allocation-free select + attend.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as murm_select_attend_fwd, without the workspace:
+ * the library keeps MURM_NOALLOC_SCRATCH_BYTES of device scratch per GPU for
+ * the life of the process and never allocates.  Shapes whose workspace
+ * (murm_select_attend_workspace_bytes) exceeds it return
+ * MURM_ERR_UNSUPPORTED.  The stream must belong to the current device.
+ * Calls on one GPU share the scratch: calls that overlap in time on one GPU
+ * (e.g. on two streams) race.
+ * ------------------------------------------------------------------------- */
+#define MURM_NOALLOC_SCRATCH_BYTES (64u << 20)
+int murm_select_attend_fwd_noalloc(int dtype, int slot_dtype, int B, int H, int N, int D, int M,
+                                   const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
+                                   const void* sk, int64_t sk_sb, int64_t sk_sh, int64_t sk_sm,
+                                   const void* sv, int64_t sv_sb, int64_t sv_sh, int64_t sv_sm,
+                                   const uint8_t* mask, int64_t mk_sb, int64_t mk_sh, int64_t mk_sn, int64_t mk_sm,
+                                   const float* bias, int64_t bs_sb, int64_t bs_sh, int64_t bs_sn, int64_t bs_sm,
+                                   int causal, double scale, int effective_M,
+                                   void* out, int64_t out_sb, int64_t out_sh, int64_t out_sn,
+                                   float* weights, int64_t* indices, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,6 +13,7 @@ from ._hip_kernels import LIB_PATH
 
 F32, F16, BF16 = 0, 1, 2
 OK, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
+NOALLOC_SCRATCH_BYTES = 64 << 20  # MURM_NOALLOC_SCRATCH_BYTES
 TIMING_CLASSES = 10
 
 _p, _i, _l, _d, _sz, _f = C.c_void_p, C.c_int, C.c_int64, C.c_double, C.c_size_t, C.c_float
@@ -50,6 +51,7 @@ SIGNATURES = {
     "murm_timing_read": (_i, [_i, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
     "murm_timing_name": (C.c_char_p, [_i]),
     "murm_selftest_mfma": (_i, [_p, _p]),
+    "murm_select_attend_fwd_noalloc": (_i, _geom + _view * 3 + _view4 * 2 + [_i, _d, _i] + _view + [_p, _p, _p]),
 }
 EXPORTS = tuple(SIGNATURES)
 
