@@ -335,6 +335,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="3", choices=sorted(list(CONFIGS) + list(MODULE_CONFIGS)))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the copy / GEMM peak measurement")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after the timed passes, copy a MIB-MiB tensor 3 times (a plain copy kernel of known "
@@ -450,7 +451,8 @@ def main():
         "kernels": kernels,
         "device_ms_per_step_in_kernels": round(device_ms, 4),
     }
-    res["measured_peaks"] = measured_peaks(torch, dev)
+    if not a.no_peaks:
+        res["measured_peaks"] = measured_peaks(torch, dev)
     if a.copy_calibration > 0:
         n = a.copy_calibration * (1 << 20) // 4
         src = torch.ones(n, device=dev)

@@ -170,6 +170,7 @@ PartParams carve_parts(Carve& c, int B, int H, int N, int D, int M, int mode) {
 struct FwdLayout {
   float* sk[MAX_ROUNDS];
   float* sv[MAX_ROUNDS];
+  void* ksp[MAX_ROUNDS];   // the round's keys split for the 16-bit select kernel
   float* ksum[MAX_ROUNDS];
   float* vsum[MAX_ROUNDS];
   float* wsum[MAX_ROUNDS];
@@ -185,6 +186,7 @@ FwdLayout fwd_layout(void* ws, int B, int H, int N, int D, int M, int R, int sha
   for (int r = 0; r < R; ++r) {
     L.sk[r] = c.take<float>(S);
     L.sv[r] = c.take<float>(S);
+    L.ksp[r] = c.take<uint16_t>(BH * ksplit_head_elems(M, pick_dp(D)));
     L.idx[r] = c.take<uint16_t>(BH * N * IDX_ROW);
     if (r < R - 1) {
       L.ksum[r] = c.take<float>(S);
@@ -232,6 +234,7 @@ BwdLayout bwd_layout(void* ws, int B, int H, int N, int D, int M, int R, int sha
 
 struct OpLayout {   // scratch of the single-round ops
   float* sk; float* sv; float* nk; float* nv;
+  void* ksp;
   float* K; float* V; float* W;
   float* dk; float* dv; float* dW; float* ck; float* cv;
   uint16_t* idx; float* ds; float* wtmp;
@@ -245,7 +248,10 @@ OpLayout op_layout(void* ws, int B, int H, int N, int D, int M, int kind) {
   const size_t BH = (size_t)B * H, S = BH * M * D;
   L.idx = c.take<uint16_t>(BH * N * IDX_ROW);
   if (kind == 0 || kind == 1 || kind == 2) { L.sk = c.take<float>(S); L.sv = c.take<float>(S); }
-  if (kind == 0) L.wtmp = c.take<float>(BH * N * KN);  // weights scratch of the select-only entry
+  if (kind == 0) {
+    L.wtmp = c.take<float>(BH * N * KN);  // weights scratch of the select-only entry
+    L.ksp = c.take<uint16_t>(BH * ksplit_head_elems(M, pick_dp(D)));
+  }
   if (kind == 1) { L.ds = c.take<float>(BH * N * KN); L.dk = c.take<float>(S); L.dv = c.take<float>(S); }
   if (kind == 2) { L.nk = c.take<float>(S); L.nv = c.take<float>(S); }
   if (kind == 3) {
@@ -263,6 +269,17 @@ int need_ws(const void* ws, size_t have, size_t need) {
   if (need > 0 && !ws) return fail(MURM_ERR_ARG, "workspace is NULL (%zu bytes needed)", need);
   if (have < need) return fail(MURM_ERR_ARG, "workspace too small: %zu < %zu bytes", have, need);
   return MURM_OK;
+}
+
+// split-key table for 16-bit tokens (the float32 select kernel reads float32 keys)
+KeySplitOut ksplit_out(int dtype, void* p, int D) {
+  KeySplitOut k{};
+  if (dtype != MURM_F32) {
+    k.p = p;
+    k.dtype = dtype;
+    k.DP = pick_dp(D);
+  }
+  return k;
 }
 
 SAParams sa_params(int B, int H, int N, int D, int M, TokView q, const float* sk, int em, int causal,
@@ -412,12 +429,14 @@ int murm_select_attend_fwd(int dtype, int slot_dtype, int B, int H, int N, int D
   {
     const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk};
     const SlotConv<const void*, float*> cb{sv, sv_sb, sv_sh, sv_sm, L.sv};
-    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+    const KeySplitOut ks = ksplit_out(dtype, L.ksp, D);
+    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st, &ks));
   }
   SAParams p = sa_params(B, H, N, D, M, tv_of(q, q_sb, q_sh, q_sn, dtype), L.sk, effective_M, causal, scale);
   p.mask = mask; p.mk_sb = mk_sb; p.mk_sh = mk_sh; p.mk_sn = mk_sn; p.mk_sm = mk_sm;
   p.bias = bias; p.bs_sb = bs_sb; p.bs_sh = bs_sh; p.bs_sn = bs_sn; p.bs_sm = bs_sm;
   p.idx16 = L.idx; p.idx64 = indices; p.w = weights;
+  p.ksplit = ksplit_out(dtype, L.ksp, D).p;
   RUN(C_SA, "select_attend", launch_select_attend(dtype, DP, p, st));
   OutParams o{};
   o.base = none_tv();
@@ -443,8 +462,13 @@ int murm_select_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, int M
   if ((rc = need_ws(workspace, workspace_bytes, L.bytes))) return rc;
   const int DP = pick_dp(D);
   hipStream_t st = (hipStream_t)stream;
-  RUN(C_CONV, "to_state", launch_to_state(slot_dtype, sk, sk_sb, sk_sh, sk_sm, L.sk, B, H, M, D, st));
+  {
+    const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk};
+    const KeySplitOut ks = ksplit_out(dtype, L.ksp, D);
+    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, nullptr, B, H, M, D, st, &ks));
+  }
   SAParams p = sa_params(B, H, N, D, M, tv_of(q, q_sb, q_sh, q_sn, dtype), L.sk, effective_M, causal, 0.0);
+  p.ksplit = ksplit_out(dtype, L.ksp, D).p;
   p.mask = mask; p.mk_sb = mk_sb; p.mk_sh = mk_sh; p.mk_sn = mk_sn; p.mk_sm = mk_sm;
   p.bias = bias; p.bs_sb = bs_sb; p.bs_sh = bs_sh; p.bs_sn = bs_sn; p.bs_sm = bs_sm;
   p.idx16 = nullptr; p.idx64 = indices;
@@ -728,12 +752,14 @@ int murm_murmurate_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
   {
     const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk[0]};
     const SlotConv<const void*, float*> cb{sv, sv_sb, sv_sh, sv_sm, L.sv[0]};
-    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st));
+    const KeySplitOut ks = ksplit_out(dtype, L.ksp[0], D);
+    RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st, &ks));
   }
   for (int r = 0; r < rounds; ++r) {
     const bool last = r == rounds - 1;
     SAParams p = sa_params(B, H, N, D, M, qv, L.sk[r], effective_M, causal, scale);
     p.mask = mask; p.mk_sb = mk_sb; p.mk_sh = mk_sh; p.mk_sn = mk_sn; p.mk_sm = mk_sm;
+    p.ksplit = ksplit_out(dtype, L.ksp[r], D).p;
     p.idx16 = L.idx[r];
     p.idx64 = last ? indices_last : nullptr;
     p.w = last ? weights_last : L.w[r];
@@ -744,6 +770,7 @@ int murm_murmurate_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
     s.sk_old = L.sk[r]; s.sv_old = L.sv[r]; s.sk_new = L.sk[r + 1]; s.sv_new = L.sv[r + 1];
     s.ksum = L.ksum[r]; s.vsum = shared ? nullptr : L.vsum[r]; s.wsum = L.wsum[r];
     s.alpha = (float)alpha; s.gamma = (float)gamma; s.diffuse = 1;
+    s.ksplit_new = ksplit_out(dtype, L.ksp[r + 1], D);
     RUN(C_SEGU, "seg_update", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, 0, st));
     if (seg_two_stage(dtype, DP, SEG_UPDATE, s, &L.part))
       RUN(C_SEGUR, "seg_update_reduce", launch_seg(dtype, DP, SEG_UPDATE, s, &L.part, 1, st));

@@ -468,10 +468,20 @@ __device__ __forceinline__ void lds8(const float* __restrict__ row, int d0, floa
 }
 
 // Blocks of the token-side kernels that stage tables: (b,h) x chunk on a 1-D
-// grid, every block of one (b,h) on XCD bh % 8 (linear id % 8 = XCD).
+// grid of 8 * ceil(BH/8) * nchunk ids.  Workgroups are dispatched round-robin
+// over the 8 XCDs (linear id % 8 = XCD): when B*H is a multiple of 8, every
+// block of one (b,h) runs on XCD bh % 8 and the head's tables reach that
+// XCD's L2 once.  Otherwise the heads would not cover the XCDs evenly, and a
+// head's chunks are simply consecutive.  Ids past the last head return.
 constexpr int TOK_XCDS = 8;
 __device__ __forceinline__ bool tok_block(int BH, int nchunk, int& bh, int& chunk) {
-  const int L = blockIdx.x, x = L % TOK_XCDS, k = L / TOK_XCDS;
+  const int L = blockIdx.x;
+  if (BH % TOK_XCDS != 0) {
+    bh = L / nchunk;
+    chunk = L % nchunk;
+    return bh < BH;
+  }
+  const int x = L % TOK_XCDS, k = L / TOK_XCDS;
   bh = x + TOK_XCDS * (k / nchunk);
   chunk = k % nchunk;
   return bh < BH;

@@ -42,6 +42,24 @@ struct SAParams {
   uint16_t* idx16;            // [BH, N, 8] or null
   int64_t* idx64;             // [BH, N, 7] or null
   float* w;                   // [BH, N, 7]
+  // 16-bit tokens: the keys already split into hi / lo halves of the token
+  // dtype in the kernel's LDS layout (KeySplit below); null: split from sk
+  const void* ksplit;
+};
+
+// Slot keys split for the 16-bit select kernel: per (b,h) a hi table then a lo
+// table, each [Mp][DP + 8] elements of the token dtype (Mp = M rounded up to
+// 16; hi = rn(k), lo = rn(k - hi); zero at d >= D and m >= M; the last 8
+// columns are row padding and never read).  This is the kernel's LDS image,
+// so the kernel copies it in with no conversion.
+__host__ __device__ inline int ksplit_row(int DP) { return DP + 8; }
+__host__ __device__ inline int ksplit_mp(int M) { return (M + 15) & ~15; }
+__host__ __device__ inline size_t ksplit_head_elems(int M, int DP) { return 2 * (size_t)ksplit_mp(M) * ksplit_row(DP); }
+
+struct KeySplitOut {   // where a kernel writes split keys (p == null: nowhere)
+  void* p;
+  int dtype;           // token dtype (DT_BF16 / DT_F16)
+  int DP;
 };
 
 struct OutParams {
@@ -68,6 +86,7 @@ struct SegParams {
   float* ksum; float* vsum; float* wsum;     // optional saved sums
   float alpha, gamma, eps;
   int diffuse;
+  KeySplitOut ksplit_new;                    // new keys, split for the next select
   // ATTBWD
   const float* carry_k; const float* carry_v;  // optional pass-through grads (read, halo included)
   int final_out;                               // 1: write G'' of the owned rows to gk_out / gv_out
@@ -179,9 +198,11 @@ struct SlotConv {   // one slot tensor [B,H,M,D] (element strides) <-> fp32 stat
   int64_t sb, sh, sm;   // strides of the slot tensor (src for to_state, dst for from_state)
   D dst;
 };
-// two conversions in one launch (b may be null)
+// two conversions in one launch (b may be null); with `split` the first one
+// (the slot keys) is also written split for the 16-bit select kernel
 hipError_t launch_to_state2(int dtype, const SlotConv<const void*, float*>& a,
-                            const SlotConv<const void*, float*>* b, int B, int H, int M, int D, hipStream_t st);
+                            const SlotConv<const void*, float*>* b, int B, int H, int M, int D, hipStream_t st,
+                            const KeySplitOut* split = nullptr);
 hipError_t launch_from_state2(int dtype, const SlotConv<const float*, void*>& a,
                               const SlotConv<const float*, void*>* b, int B, int H, int M, int D, hipStream_t st);
 hipError_t launch_to_state(int dtype, const void* src, int64_t sb, int64_t sh, int64_t sm, float* dst,

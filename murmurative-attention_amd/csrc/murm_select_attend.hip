@@ -106,27 +106,35 @@ __device__ __forceinline__ V load_operand8(const T* row, int d0, int D, bool vec
   return v;
 }
 
+// Blocks of the select kernels: (b,h) x token chunk as tok_block maps them
+// (with B*H a multiple of 8 all blocks of a head share one XCD's L2, where
+// the head's slot keys then arrive once).
+__device__ __forceinline__ bool sa_block(int BH, int nchunk, int& bh, int& chunk) {
+  return tok_block(BH, nchunk, bh, chunk);
+}
+
 // ---------------------------------------------------------------------------
 // 16-bit tokens (bf16 / fp16): hi/lo split keys in LDS, 16x16x32 MFMA
 // ---------------------------------------------------------------------------
 template <typename T, int DP, bool WIDE>
-__global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
+__global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p, int nchunk) {
   using V = typename Mfma16<T>::vec;
   constexpr int G = SAShape<DP>::G;
   constexpr int KC = DP / 32;
-  constexpr int ROW = DP + 8;  // LDS row stride in elements (16 B pad)
+  constexpr int ROW = DP + 8;  // LDS row stride in elements (16 B pad); = ksplit_row(DP)
   extern __shared__ __align__(16) unsigned char smem[];
   T* lhi = reinterpret_cast<T*>(smem);
   const int Mp = (p.M + 15) & ~15;
   T* llo = lhi + Mp * ROW;
 
-  const int bh = blockIdx.y;
+  int bh, chunk;
+  if (!sa_block(p.B * p.H, nchunk, bh, chunk)) return;
   const int b = bh / p.H, h = bh % p.H;
   const float* skb = p.sk + (int64_t)bh * p.M * p.D;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int quad = lane >> 4, col = lane & 15;
-  const int tok0 = blockIdx.x * SAShape<DP, SA16_WAVES>::TOK + wave * (G * 16);
+  const int tok0 = chunk * SAShape<DP, SA16_WAVES>::TOK + wave * (G * 16);
 
   // WIDE (16-byte aligned rows, D % 8 == 0): the wave's token rows are
   // requested before the keys are staged, unconditionally from clamped rows
@@ -142,10 +150,15 @@ __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
     }
   }
 
-  // stage the keys: batches of STB float4 loads in flight per thread, then
-  // the hi/lo split written as 8-byte LDS stores
+  // stage the keys: the pre-split table is copied in as it lies (global ->
+  // LDS, no registers); otherwise batches of STB float4 loads in flight per
+  // thread, then the hi/lo split written as 8-byte LDS stores
   constexpr int STB = 8;
-  const int nq = Mp * (DP / 4);
+  const int nq = p.ksplit ? 0 : Mp * (DP / 4);
+  if (p.ksplit) {
+    const size_t head = 2 * (size_t)Mp * ROW;
+    copy_to_lds(lhi, reinterpret_cast<const T*>(p.ksplit) + (size_t)bh * head, (int)(head * sizeof(T)));
+  }
   const bool vec4 = (p.D & 3) == 0;
   for (int i0 = threadIdx.x; i0 < nq; i0 += STB * blockDim.x) {
     float4 v[STB];
@@ -317,7 +330,7 @@ __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p) {
 // float32 tokens: f32 keys in LDS, 16x16x4 f32 MFMA, exact softmax scores
 // ---------------------------------------------------------------------------
 template <int DP>
-__global__ __launch_bounds__(256) void sa_kernel32(SAParams p) {
+__global__ __launch_bounds__(256) void sa_kernel32(SAParams p, int nchunk) {
   constexpr int G = SAShape<DP>::G;
   constexpr int KK = DP / 4;
   constexpr int ROW = DP + 4;
@@ -325,7 +338,8 @@ __global__ __launch_bounds__(256) void sa_kernel32(SAParams p) {
   float* lsk = reinterpret_cast<float*>(smem);
   const int Mp = (p.M + 15) & ~15;
 
-  const int bh = blockIdx.y;
+  int bh, chunk;
+  if (!sa_block(p.B * p.H, nchunk, bh, chunk)) return;
   const int b = bh / p.H, h = bh % p.H;
   const float* skb = p.sk + (int64_t)bh * p.M * p.D;
   constexpr int STB = 8;
@@ -363,7 +377,7 @@ __global__ __launch_bounds__(256) void sa_kernel32(SAParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int quad = lane >> 4, col = lane & 15;
-  const int tok0 = blockIdx.x * SAShape<DP>::TOK + wave * (G * 16);
+  const int tok0 = chunk * SAShape<DP>::TOK + wave * (G * 16);
   if (tok0 >= p.N) return;
 
   float bq[G][KK];
@@ -565,12 +579,17 @@ __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p,
   }
 }
 
+// 1-D grid of sa_block (tok_block ids)
+inline dim3 sa_grid(int BH, int nchunk) { return dim3(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk); }
+
 template <typename T, int DP>
 hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
   const int Mp = (p.M + 15) & ~15;
+  const int BH = p.B * p.H;
   if constexpr (sizeof(T) == 2) {
     using S = SAShape<DP, SA16_WAVES>;
-    dim3 grid((p.N + S::TOK - 1) / S::TOK, p.B * p.H);
+    const int nchunk = (p.N + S::TOK - 1) / S::TOK;
+    const dim3 grid = sa_grid(BH, nchunk);
     const size_t lds = 2 * (size_t)Mp * (DP + 8) * sizeof(T);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     const bool wide = p.q.vec && p.D % 8 == 0;
@@ -579,17 +598,19 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     if (wide)
-      MURM_LAUNCH((sa_kernel16<T, DP, true>), grid, dim3(64 * SA16_WAVES), lds, st, p);
+      MURM_LAUNCH((sa_kernel16<T, DP, true>), grid, dim3(64 * SA16_WAVES), lds, st, p, nchunk);
     else
-      MURM_LAUNCH((sa_kernel16<T, DP, false>), grid, dim3(64 * SA16_WAVES), lds, st, p);
+      MURM_LAUNCH((sa_kernel16<T, DP, false>), grid, dim3(64 * SA16_WAVES), lds, st, p, nchunk);
   } else {
-    dim3 grid((p.N + SAShape<DP>::TOK - 1) / SAShape<DP>::TOK, p.B * p.H);
+    if (p.ksplit) return hipErrorInvalidValue;  // float32 tokens use the float32 keys
+    const int nchunk = (p.N + SAShape<DP>::TOK - 1) / SAShape<DP>::TOK;
+    const dim3 grid = sa_grid(BH, nchunk);
     const size_t lds = (size_t)Mp * (DP + 4) * sizeof(float);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sa_kernel32<DP>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    MURM_LAUNCH((sa_kernel32<DP>), grid, dim3(256), lds, st, p);
+    MURM_LAUNCH((sa_kernel32<DP>), grid, dim3(256), lds, st, p, nchunk);
   }
   return hipGetLastError();
 }

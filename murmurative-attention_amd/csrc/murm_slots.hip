@@ -64,6 +64,23 @@ __device__ __forceinline__ void load_old(const SegParams& p, int bh, int lo, int
   }
 }
 
+// hi + lo halves of a float32 key in the token dtype TT, stored into the
+// split-key table (KeySplit layout: hi table, then lo table, rows of DP + 8)
+template <typename TT>
+__device__ __forceinline__ void put_split(TT* head, int Mp, int row, int m, int d, float v) {
+  const TT hi = (TT)v;
+  head[(size_t)m * row + d] = hi;
+  head[((size_t)Mp + m) * row + d] = (TT)(v - (float)hi);
+}
+__device__ __forceinline__ void put_split_dt(const KeySplitOut& ks, int bh, int M, int m, int d, float v) {
+  const int Mp = ksplit_mp(M), row = ksplit_row(ks.DP);
+  const size_t head = (size_t)bh * ksplit_head_elems(M, ks.DP);
+  if (ks.dtype == DT_BF16)
+    put_split(static_cast<__bf16*>(ks.p) + head, Mp, row, m, d, v);
+  else
+    put_split(static_cast<_Float16*>(ks.p) + head, Mp, row, m, d, v);
+}
+
 template <int DP>
 __device__ void update_epilogue(const SegParams& p, int bh, int g0, int halo, int NS, float* accA, float* accB,
                                 const float* accW, const OldState& os) {
@@ -99,17 +116,25 @@ __device__ void update_epilogue(const SegParams& p, int bh, int g0, int halo, in
   }
   __syncthreads();
   const float gm = p.gamma;
+  // owned rows; with a split-key output also its zero padding (d >= D, and
+  // rows M..Mp-1, which fall in the last slot group)
+  const int Mp = ksplit_mp(p.M);
   for (int i = threadIdx.x; i < GS * DP; i += blockDim.x) {
     const int own = i / DP, d = i % DP, m = g0 + own;
-    if (m >= p.M || d >= p.D) continue;
-    const int rel = own + halo;
-    float yk = accA[rel * DP + d], yv = accB[rel * DP + d];
-    if (p.diffuse && m >= 1 && m <= p.M - 2) {
-      yk = yk + gm * (accA[(rel - 1) * DP + d] + accA[(rel + 1) * DP + d] - 2.0f * yk);
-      yv = yv + gm * (accB[(rel - 1) * DP + d] + accB[(rel + 1) * DP + d] - 2.0f * yv);
+    if (m >= Mp) continue;
+    float yk = 0.f;
+    if (m < p.M && d < p.D) {
+      const int rel = own + halo;
+      yk = accA[rel * DP + d];
+      float yv = accB[rel * DP + d];
+      if (p.diffuse && m >= 1 && m <= p.M - 2) {
+        yk = yk + gm * (accA[(rel - 1) * DP + d] + accA[(rel + 1) * DP + d] - 2.0f * yk);
+        yv = yv + gm * (accB[(rel - 1) * DP + d] + accB[(rel + 1) * DP + d] - 2.0f * yv);
+      }
+      p.sk_new[base + (int64_t)m * p.D + d] = yk;
+      p.sv_new[base + (int64_t)m * p.D + d] = yv;
     }
-    p.sk_new[base + (int64_t)m * p.D + d] = yk;
-    p.sv_new[base + (int64_t)m * p.D + d] = yv;
+    if (p.ksplit_new.p) put_split_dt(p.ksplit_new, bh, p.M, m, d, yk);
   }
 }
 
@@ -1008,6 +1033,49 @@ __global__ void to_state4_kernel(SlotConv<const T*, float*> c0, SlotConv<const T
   }
 }
 
+// The same conversion with the keys (blockIdx.y == 0) also written split for
+// the 16-bit select kernel: the keys' items run over every element of the
+// split table (Mp rows of DP dims, zero past M and D), the values' over the
+// tensor as to_state4_kernel does.
+template <typename T, typename TT>
+__global__ void to_state_split_kernel(SlotConv<const T*, float*> ck, SlotConv<const T*, float*> cv, TT* split,
+                                      int H, int M, int D, int DP, int total_k, int total_v) {
+  const int D4 = (D + 3) >> 2;
+  if (blockIdx.y == 1) {
+    for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < total_v; q += gridDim.x * blockDim.x) {
+      const int row = q / D4, d0 = (q - row * D4) * 4;
+      const int bh = row / M, m = row - bh * M, b = bh / H, h = bh - b * H;
+      const T* sp = cv.src + b * cv.sb + h * cv.sh + (int64_t)m * cv.sm + d0;
+      float* o = cv.dst + (int64_t)row * D + d0;
+      for (int e = 0; e < 4 && d0 + e < D; ++e) o[e] = to_f(sp[e]);
+    }
+    return;
+  }
+  const int Mp = ksplit_mp(M), srow = ksplit_row(DP), DP4 = DP / 4;
+  for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < total_k; q += gridDim.x * blockDim.x) {
+    const int row = q / DP4, d0 = (q - row * DP4) * 4;
+    const int bh = row / Mp, m = row - bh * Mp, b = bh / H, h = bh - b * H;
+    float f[4] = {0.f, 0.f, 0.f, 0.f};
+    if (m < M) {
+      const T* sp = ck.src + b * ck.sb + h * ck.sh + (int64_t)m * ck.sm + d0;
+      float* o = ck.dst + ((int64_t)bh * M + m) * D + d0;
+      for (int e = 0; e < 4 && d0 + e < D; ++e) {
+        f[e] = to_f(sp[e]);
+        o[e] = f[e];
+      }
+    }
+    TT hi[4], lo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hi[e] = (TT)f[e];
+      lo[e] = (TT)(f[e] - (float)hi[e]);
+    }
+    TT* head = split + (size_t)bh * ksplit_head_elems(M, DP);
+    *reinterpret_cast<uint2*>(head + (size_t)m * srow + d0) = *reinterpret_cast<const uint2*>(hi);
+    *reinterpret_cast<uint2*>(head + ((size_t)Mp + m) * srow + d0) = *reinterpret_cast<const uint2*>(lo);
+  }
+}
+
 template <typename T>
 __global__ void from_state4_kernel(SlotConv<const float*, T*> c0, SlotConv<const float*, T*> c1, int H, int M,
                                    int D, int total4) {
@@ -1266,13 +1334,41 @@ hipError_t launch_du(const DuParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <typename T, typename TT>
+hipError_t launch_split_t(const SlotConv<const T*, float*>& a, const SlotConv<const T*, float*>& b, bool has_b,
+                          const KeySplitOut& ks, int B, int H, int M, int D, hipStream_t st) {
+  const int64_t tk = (int64_t)B * H * ksplit_mp(M) * (ks.DP / 4);
+  const int64_t tv = has_b ? (int64_t)B * H * M * ((D + 3) / 4) : 0;
+  if (tk >= (int64_t(1) << 30) || tv >= (int64_t(1) << 30)) return hipErrorInvalidValue;
+  const dim3 grid(grid1d(tk > tv ? tk : tv), has_b ? 2 : 1);
+  MURM_LAUNCH((to_state_split_kernel<T, TT>), grid, dim3(256), 0, st, a, b, static_cast<TT*>(ks.p), H, M, D, ks.DP,
+              (int)tk, (int)tv);
+  return hipGetLastError();
+}
+
 hipError_t launch_to_state2(int dtype, const SlotConv<const void*, float*>& a,
-                            const SlotConv<const void*, float*>* bp, int B, int H, int M, int D, hipStream_t st) {
+                            const SlotConv<const void*, float*>* bp, int B, int H, int M, int D, hipStream_t st,
+                            const KeySplitOut* split) {
   const SlotConv<const void*, float*> bb = bp ? *bp : a;
   auto cv = [](const SlotConv<const void*, float*>& c, auto* tag) {
     using T = std::remove_const_t<std::remove_pointer_t<decltype(tag)>>;
     return SlotConv<const T*, float*>{static_cast<const T*>(c.src), c.sb, c.sh, c.sm, c.dst};
   };
+  if (split && split->p) {
+    auto go = [&](auto* tag) -> hipError_t {
+      using T = std::remove_const_t<std::remove_pointer_t<decltype(tag)>>;
+      const auto ca = cv(a, (const T*)nullptr), cb = cv(bb, (const T*)nullptr);
+      if (split->dtype == DT_BF16) return launch_split_t<T, __bf16>(ca, cb, bp != nullptr, *split, B, H, M, D, st);
+      if (split->dtype == DT_F16) return launch_split_t<T, _Float16>(ca, cb, bp != nullptr, *split, B, H, M, D, st);
+      return hipErrorInvalidValue;
+    };
+    switch (dtype) {
+      case DT_BF16: return go((const __bf16*)nullptr);
+      case DT_F16: return go((const _Float16*)nullptr);
+      case DT_F32: return go((const float*)nullptr);
+      default: return hipErrorInvalidValue;
+    }
+  }
   const int64_t total4 = (int64_t)B * H * M * ((D + 3) / 4);
   if (total4 < (int64_t(1) << 30)) {  // 32-bit indices, grid-stride step included
     const dim3 g4(grid1d(total4), bp ? 2 : 1);
