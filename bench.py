@@ -2,8 +2,9 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu]
 
---config 2/3/4 run the op on BASELINE.json configs[1..3]; --config 5 runs the
-README MurmurativeAttention layer's training step.
+--config 1/2/3/4 run the op on BASELINE.json configs[0..3] (config 1, the
+README verify call, forward + backward here); --config 5 runs the README
+MurmurativeAttention layer's training step.
 
 A step is one forward+backward of the README-form slot_murmurate over one
 synthetic batch (seeded N(0,1) draws), inputs resident
@@ -18,6 +19,7 @@ beside the spec peaks.  Prints one JSON line.
 """
 
 import argparse
+import contextlib
 import json
 import math
 import os
@@ -36,6 +38,9 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 CONFIGS = {
     # name: (B, H, N, D, M, rounds, causal, dtype, slots_k std, slots_v std)
+    # config 1 is the README verify call (forward, fp32); here it is timed
+    # forward + backward like the others
+    "1": (2, 4, 128, 64, 256, 3, False, "float32", 1.0, 0.0),
     "2": (4, 8, 2048, 64, 256, 3, False, "float16", 1.0, 0.02),
     "3": (1, 16, 8192, 64, 256, 3, False, "bfloat16", 1.0, 0.02),
     "4": (1, 16, 65536, 128, 256, 3, True, "bfloat16", 1.0, 0.02),
@@ -336,6 +341,8 @@ def main():
     ap.add_argument("--config", default="3", choices=sorted(list(CONFIGS) + list(MODULE_CONFIGS)))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-peaks", action="store_true", help="skip the copy / GEMM peak measurement")
+    ap.add_argument("--graphs", action="store_true",
+                    help="replay the fused rounds' kernels from captured hipGraphs (murm_graph_replay)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after the timed passes, copy a MIB-MiB tensor 3 times (a plain copy kernel of known "
@@ -352,6 +359,7 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
+    capi.graph_replay(a.graphs)
     module = a.config in MODULE_CONFIGS
     if module:
         mc = MODULE_CONFIGS[a.config]
@@ -372,14 +380,18 @@ def main():
             out, idx, w = murmurative.slot_murmurate(q, sk, sv, rounds=R, causal=causal)
             return torch.autograd.grad(out, (q, sk, sv), go)
 
-    for _ in range(a.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(a.steps):
-        step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    # graph capture needs a stream other than the legacy null stream torch
+    # runs on by default (default priority)
+    side = torch.cuda.Stream() if a.graphs else None
+    with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
+        for _ in range(a.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
     ms_per_step = 1e3 * elapsed / a.steps
     value = B * N * a.steps / elapsed
 
@@ -446,6 +458,7 @@ def main():
         "metric": metric, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": dname, "data": data, "config": config,
+        "launches": "hipGraph replay (murm_graph_replay)" if a.graphs else "direct kernel launches",
         "roofline": roofline,
         "call_roofline": call_roofline,
         "kernels": kernels,

@@ -260,6 +260,20 @@ int murm_murmurate_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Graph replay of the fused rounds (no counterpart in the reference, whose
+ * slot_murmurate issues its rounds op by op from Python, ops.py:376-419).
+ * With replay on, murm_murmurate_fwd / murm_murmurate_bwd capture their
+ * kernel sequence for each distinct argument set (pointers, sizes, scalars,
+ * stream) into a hipGraph once and replay it with one hipGraphLaunch after
+ * that (at most 16 cached graphs, least recently used dropped).  Calls on
+ * the null stream, calls while timing is on, and calls on a stream that is
+ * already being captured launch their kernels directly.  Turning replay off
+ * destroys the cached graphs.  murm_graph_cached returns their number.
+ * ------------------------------------------------------------------------- */
+void murm_graph_replay(int on);
+int murm_graph_cached(void);
+
+/* ---------------------------------------------------------------------------
  * Measurement hooks (no counterpart in the reference).  When enabled, every
  * kernel launch records a start and a stop HIP event from its own dispatch
  * (hipExtLaunchKernel), so each pair times the kernel's execution alone;

@@ -346,6 +346,90 @@ __global__ void selftest_mfma_kernel(float* out) {
   }
 }
 
+// ------------------------------------------------------- graph replay ---
+// Opt-in (murm_graph_replay): the fused rounds' launch sequence of each
+// distinct argument set (every pointer, size and scalar, and the stream) is
+// captured once into a hipGraph and replayed with one hipGraphLaunch after
+// that.  Skipped when timing is on, on the null stream, and when the stream
+// is already capturing (the launches then join the caller's graph).
+struct GraphCache {
+  std::mutex mu;
+  bool on = false;
+  struct Entry {
+    std::string key;
+    hipGraphExec_t exec;
+  };
+  std::vector<Entry> entries;  // most recent last
+  static constexpr size_t CAP = 16;
+};
+GraphCache& graphs() {
+  static GraphCache g;
+  return g;
+}
+
+template <typename... A>
+std::string graph_key(char tag, const A&... args) {
+  std::string k(1, tag);
+  (k.append(reinterpret_cast<const char*>(&args), sizeof(args)), ...);
+  return k;
+}
+
+// Runs `enqueue` on st directly, or through a cached (or newly captured) graph.
+template <typename F>
+int with_graph(hipStream_t st, const std::string& key, F&& enqueue) {
+  GraphCache& G = graphs();
+  bool on;
+  {
+    std::lock_guard<std::mutex> lk(G.mu);
+    on = G.on;
+  }
+  {
+    std::lock_guard<std::mutex> lk(timing().mu);
+    on = on && !timing().on;
+  }
+  if (on && st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) on = false;
+  }
+  if (!on || !st) return enqueue();
+  hipGraphExec_t exec = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(G.mu);
+    for (size_t i = 0; i < G.entries.size(); ++i) {
+      if (G.entries[i].key == key) {
+        GraphCache::Entry e = G.entries[i];
+        G.entries.erase(G.entries.begin() + i);
+        G.entries.push_back(e);
+        exec = e.exec;
+        break;
+      }
+    }
+  }
+  if (!exec) {
+    hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return fail(MURM_ERR_HIP, "hipStreamBeginCapture: %s", hipGetErrorString(e));
+    const int rc = enqueue();
+    hipGraph_t g = nullptr;
+    e = hipStreamEndCapture(st, &g);
+    if (rc != MURM_OK) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    if (e != hipSuccess || !g) return fail(MURM_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail(MURM_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lk(G.mu);
+    if (G.entries.size() >= GraphCache::CAP) {
+      (void)hipGraphExecDestroy(G.entries.front().exec);
+      G.entries.erase(G.entries.begin());
+    }
+    G.entries.push_back({key, exec});
+  }
+  const hipError_t e = hipGraphLaunch(exec, st);
+  return e == hipSuccess ? MURM_OK : fail(MURM_ERR_HIP, "hipGraphLaunch: %s", hipGetErrorString(e));
+}
+
 }  // namespace
 
 namespace murm {
@@ -726,8 +810,8 @@ size_t murm_murmurate_workspace_bytes(int B, int H, int N, int D, int M, int rou
   return fwd_layout(nullptr, B, H, N, D, M, rounds, shared_kv).bytes;
 }
 
-int murm_murmurate_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, int M, int rounds, double alpha,
-                       double gamma, int causal, int effective_M, double scale, const void* q, int64_t q_sb,
+static int murmurate_fwd_enqueue(int dtype, int slot_dtype, int B, int H, int N, int D, int M, int rounds,
+                       double alpha, double gamma, int causal, int effective_M, double scale, const void* q, int64_t q_sb,
                        int64_t q_sh, int64_t q_sn, const void* x, int64_t x_sb, int64_t x_sh, int64_t x_sn,
                        const void* tk, int64_t tk_sb, int64_t tk_sh, int64_t tk_sn, const void* tv,
                        int64_t tv_sb, int64_t tv_sh, int64_t tv_sn, const void* sk, int64_t sk_sb, int64_t sk_sh,
@@ -812,8 +896,8 @@ size_t murm_murmurate_bwd_workspace_bytes(int B, int H, int N, int D, int M, int
   return bwd_layout(nullptr, B, H, N, D, M, rounds, shared_kv).bytes;
 }
 
-int murm_murmurate_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, int M, int rounds, double alpha,
-                       double gamma, double scale, int x_given, const void* grad_out, int64_t g_sb, int64_t g_sh,
+static int murmurate_bwd_enqueue(int dtype, int slot_dtype, int B, int H, int N, int D, int M, int rounds,
+                       double alpha, double gamma, double scale, int x_given, const void* grad_out, int64_t g_sb, int64_t g_sh,
                        int64_t g_sn, const float* grad_weights_last, const void* q, int64_t q_sb, int64_t q_sh,
                        int64_t q_sn, const void* tk, int64_t tk_sb, int64_t tk_sh, int64_t tk_sn, const void* tv,
                        int64_t tv_sb, int64_t tv_sh, int64_t tv_sn, const float* weights_last,
@@ -893,6 +977,69 @@ int murm_murmurate_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, in
   }
   RUN(C_TOKG, "tok_grad", launch_tok_grad(dtype, DP, tg, st));
   return MURM_OK;
+}
+
+int murm_murmurate_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, int M, int rounds, double alpha,
+                       double gamma, int causal, int effective_M, double scale, const void* q, int64_t q_sb,
+                       int64_t q_sh, int64_t q_sn, const void* x, int64_t x_sb, int64_t x_sh, int64_t x_sn,
+                       const void* tk, int64_t tk_sb, int64_t tk_sh, int64_t tk_sn, const void* tv,
+                       int64_t tv_sb, int64_t tv_sh, int64_t tv_sn, const void* sk, int64_t sk_sb, int64_t sk_sh,
+                       int64_t sk_sm, const void* sv, int64_t sv_sb, int64_t sv_sh, int64_t sv_sm,
+                       const uint8_t* mask, int64_t mk_sb, int64_t mk_sh, int64_t mk_sn, int64_t mk_sm, void* out,
+                       int64_t out_sb, int64_t out_sh, int64_t out_sn, int64_t* indices_last,
+                       float* weights_last, void* workspace, size_t workspace_bytes, void* stream) {
+  const std::string key =
+      graph_key('f', dtype, slot_dtype, B, H, N, D, M, rounds, alpha, gamma, causal, effective_M, scale, q, q_sb,
+                q_sh, q_sn, x, x_sb, x_sh, x_sn, tk, tk_sb, tk_sh, tk_sn, tv, tv_sb, tv_sh, tv_sn, sk, sk_sb, sk_sh,
+                sk_sm, sv, sv_sb, sv_sh, sv_sm, mask, mk_sb, mk_sh, mk_sn, mk_sm, out, out_sb, out_sh, out_sn,
+                indices_last, weights_last, workspace, workspace_bytes, stream);
+  return with_graph((hipStream_t)stream, key, [&]() {
+    return murmurate_fwd_enqueue(dtype, slot_dtype, B, H, N, D, M, rounds, alpha, gamma, causal, effective_M, scale,
+                                 q, q_sb, q_sh, q_sn, x, x_sb, x_sh, x_sn, tk, tk_sb, tk_sh, tk_sn, tv, tv_sb, tv_sh,
+                                 tv_sn, sk, sk_sb, sk_sh, sk_sm, sv, sv_sb, sv_sh, sv_sm, mask, mk_sb, mk_sh, mk_sn,
+                                 mk_sm, out, out_sb, out_sh, out_sn, indices_last, weights_last, workspace,
+                                 workspace_bytes, stream);
+  });
+}
+
+int murm_murmurate_bwd(int dtype, int slot_dtype, int B, int H, int N, int D, int M, int rounds, double alpha,
+                       double gamma, double scale, int x_given, const void* grad_out, int64_t g_sb, int64_t g_sh,
+                       int64_t g_sn, const float* grad_weights_last, const void* q, int64_t q_sb, int64_t q_sh,
+                       int64_t q_sn, const void* tk, int64_t tk_sb, int64_t tk_sh, int64_t tk_sn, const void* tv,
+                       int64_t tv_sb, int64_t tv_sh, int64_t tv_sn, const float* weights_last,
+                       const void* fwd_workspace, size_t fwd_workspace_bytes, void* grad_q, int64_t gq_sb,
+                       int64_t gq_sh, int64_t gq_sn, void* grad_tk, int64_t gtk_sb, int64_t gtk_sh,
+                       int64_t gtk_sn, void* grad_tv, int64_t gtv_sb, int64_t gtv_sh, int64_t gtv_sn,
+                       void* grad_sk, void* grad_sv, void* workspace, size_t workspace_bytes, void* stream) {
+  const std::string key =
+      graph_key('b', dtype, slot_dtype, B, H, N, D, M, rounds, alpha, gamma, scale, x_given, grad_out, g_sb, g_sh,
+                g_sn, grad_weights_last, q, q_sb, q_sh, q_sn, tk, tk_sb, tk_sh, tk_sn, tv, tv_sb, tv_sh, tv_sn,
+                weights_last, fwd_workspace, fwd_workspace_bytes, grad_q, gq_sb, gq_sh, gq_sn, grad_tk, gtk_sb,
+                gtk_sh, gtk_sn, grad_tv, gtv_sb, gtv_sh, gtv_sn, grad_sk, grad_sv, workspace, workspace_bytes,
+                stream);
+  return with_graph((hipStream_t)stream, key, [&]() {
+    return murmurate_bwd_enqueue(dtype, slot_dtype, B, H, N, D, M, rounds, alpha, gamma, scale, x_given, grad_out,
+                                 g_sb, g_sh, g_sn, grad_weights_last, q, q_sb, q_sh, q_sn, tk, tk_sb, tk_sh, tk_sn,
+                                 tv, tv_sb, tv_sh, tv_sn, weights_last, fwd_workspace, fwd_workspace_bytes, grad_q,
+                                 gq_sb, gq_sh, gq_sn, grad_tk, gtk_sb, gtk_sh, gtk_sn, grad_tv, gtv_sb, gtv_sh,
+                                 gtv_sn, grad_sk, grad_sv, workspace, workspace_bytes, stream);
+  });
+}
+
+void murm_graph_replay(int on) {
+  GraphCache& G = graphs();
+  std::lock_guard<std::mutex> lk(G.mu);
+  G.on = on != 0;
+  if (!G.on) {
+    for (auto& e : G.entries) (void)hipGraphExecDestroy(e.exec);
+    G.entries.clear();
+  }
+}
+
+int murm_graph_cached(void) {
+  GraphCache& G = graphs();
+  std::lock_guard<std::mutex> lk(G.mu);
+  return (int)G.entries.size();
 }
 
 }  // extern "C"

@@ -1232,22 +1232,30 @@ bool part_ok(const SegParams& p, int mode, const PartParams* pp, int& nvec, int&
 // 32 (and the sub-chunk's staging latency per token) within the LDS budget.
 constexpr int MSUBT = 64;
 
+// stage 1 of every token-chunk path: chunk sums in chunk order + epilogue
+template <int DP>
+hipError_t launch_reduce(int mode, const SegParams& p, const PartParams& pp, hipStream_t st) {
+  const int BH = p.B * p.H;
+  const int G = (p.M + GS - 1) / GS;
+  const dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * G);
+  if (mode == SEG_ATTBWD)
+    MURM_LAUNCH((seg_reduce_kernel<DP, SEG_ATTBWD>), grid, dim3(red_threads(pp.nchunk, DP)), 0, st, p, pp);
+  else
+    MURM_LAUNCH((seg_reduce_kernel<DP, SEG_UPDATE>), grid, dim3(red_threads(pp.nchunk, DP)), 0, st, p, pp);
+  return hipGetLastError();
+}
+
 template <typename T, int DP, int MODE, int NV, int TG>
 hipError_t launch_mma(const SegParams& p, const PartParams& pp, int stage, hipStream_t st) {
   using Sh = MmaShape<DP, MODE, NV, MSUBT, TG>;
   const int BH = p.B * p.H;
-  if (stage == 0) {
-    const void* fn = reinterpret_cast<const void*>(&seg_mma_kernel<T, DP, MODE, NV, MSUBT, TG>);
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Sh::LDS);
-    if (e != hipSuccess) return e;
-    const int nsg = (p.M + Sh::MS - 1) / Sh::MS;
-    dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk * nsg);
-    MURM_LAUNCH((seg_mma_kernel<T, DP, MODE, NV, MSUBT, TG>), grid, dim3(Sh::THREADS), Sh::LDS, st, p, pp);
-  } else {
-    const int G = (p.M + GS - 1) / GS;
-    MURM_LAUNCH((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G),
-                       dim3(red_threads(pp.nchunk, DP)), 0, st, p, pp);
-  }
+  if (stage != 0) return launch_reduce<DP>(MODE, p, pp, st);
+  const void* fn = reinterpret_cast<const void*>(&seg_mma_kernel<T, DP, MODE, NV, MSUBT, TG>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)Sh::LDS);
+  if (e != hipSuccess) return e;
+  const int nsg = (p.M + Sh::MS - 1) / Sh::MS;
+  dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * pp.nchunk * nsg);
+  MURM_LAUNCH((seg_mma_kernel<T, DP, MODE, NV, MSUBT, TG>), grid, dim3(Sh::THREADS), Sh::LDS, st, p, pp);
   return hipGetLastError();
 }
 

@@ -46,6 +46,8 @@ SIGNATURES = {
     "murm_murmurate_bwd_workspace_bytes": (_sz, [_i] * 7),
     "murm_murmurate_bwd": (_i, [_i] * 8 + [_d, _d, _d, _i] + _view + [_p] + _view * 3 + [_p, _p, _sz]
                            + _view * 3 + [_p, _p, _p, _sz, _p]),
+    "murm_graph_replay": (None, [_i]),
+    "murm_graph_cached": (_i, []),
     "murm_timing_enable": (None, [_i]),
     "murm_timing_reset": (None, []),
     "murm_timing_read": (_i, [_i, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
@@ -78,6 +80,11 @@ def check(rc: int, what: str = "murmurative_hip"):
     if rc != OK:
         msg = load().murm_last_error().decode(errors="replace")
         raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def graph_replay(on: bool = True):
+    """Replay the fused rounds' kernels from captured hipGraphs (see the header)."""
+    load().murm_graph_replay(1 if on else 0)
 
 
 def timing_enable(on: bool = True):
