@@ -518,14 +518,22 @@ struct MmaShape {
   static constexpr int DT = DP / 16;                        // dim tiles
   static constexpr int KINDS = MODE == SEG_ATTBWD ? 2 : 1;  // coefficient kinds (c*ds, w)
   static constexpr int WTILE = MODE == SEG_UPDATE ? 1 : 0;  // ones tile for the weight sums
-  static constexpr int WT = 256 / DP;                       // slot tiles per wave: 64 accumulators
   static constexpr int ROWB = SUBT * 2;
-  static constexpr int MS_REG = MMA_WAVES * WT * 16;
-  // C^T in what is left of 144 KiB (per token group) after the token rows,
+  // The attend backward (d <= 64) sizes its slot group for two blocks per CU
+  // (80 KiB of LDS, 128 VGPRs each), so one block's staging and marking run
+  // beside the other's products; the other forms run one block per CU (the
+  // update with one vector as a ping-pong pair of token groups).
+  static constexpr int BLOCKS_PER_CU = MODE == SEG_ATTBWD && DP <= 64 ? 2 : 1;
+  static constexpr int BUDGET = BLOCKS_PER_CU == 2 ? 80 * 1024 : 144 * 1024;
+  // C^T in what is left of the budget (per token group) after the token rows,
   // in whole groups of MMA_WAVES tiles
   static constexpr int MS_LDS =
-      (((144 * 1024) / TG - NV * DP * ROWB) / (KINDS * 2 * ROWB)) / (MMA_WAVES * 16) * (MMA_WAVES * 16);
+      ((BUDGET / TG - NV * DP * ROWB) / (KINDS * 2 * ROWB)) / (MMA_WAVES * 16) * (MMA_WAVES * 16);
+  // slot tiles per wave: at most 64 accumulators
+  static constexpr int WT = 256 / DP < MS_LDS / (MMA_WAVES * 16) ? 256 / DP : MS_LDS / (MMA_WAVES * 16);
+  static constexpr int MS_REG = MMA_WAVES * WT * 16;
   static constexpr int MS = MS_REG < MS_LDS ? MS_REG : MS_LDS;    // slots per block
+  static constexpr int WAVES_PER_EU = BLOCKS_PER_CU * (64 * MMA_WAVES * NV * TG / 64) / 4;
   static constexpr size_t GLDS = (size_t)NV * DP * ROWB + (size_t)KINDS * 2 * MS * ROWB;  // per group
   static constexpr int NACC = WT * DT + WTILE * WT;         // float4 accumulators per thread
   static constexpr size_t MERGE = TG > 1 ? (size_t)NACC * GT * 16 : 0;
@@ -533,7 +541,8 @@ struct MmaShape {
 };
 
 template <typename T, int DP, int MODE, int NV, int SUBT, int TG>
-__global__ __launch_bounds__(64 * MMA_WAVES * NV * TG, 2) void seg_mma_kernel(SegParams p, PartParams pp) {
+__global__ __launch_bounds__(64 * MMA_WAVES * NV * TG, (MmaShape<DP, MODE, NV, SUBT, TG>::WAVES_PER_EU))
+void seg_mma_kernel(SegParams p, PartParams pp) {
   using V = typename Mfma16<T>::vec;
   using Sh = MmaShape<DP, MODE, NV, SUBT, TG>;
   constexpr int DT = Sh::DT, KINDS = Sh::KINDS, WT = Sh::WT, MS = Sh::MS, ROWB = Sh::ROWB;
