@@ -1,6 +1,8 @@
 // Kernel parameter blocks and launchers (internal to libmurmurative_hip).
 #pragma once
 
+#include <atomic>
+
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -152,6 +154,26 @@ struct AttendIdxParams {
   float scale;
   float* w;               // [BH, N, 7]
 };
+
+// Compute units of the current device (cached per device; 256 if the query
+// fails).  Launchers shrink their blocks when a grid would leave CUs idle.
+inline int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) {
+      (void)hipGetLastError();
+      c = 256;
+    }
+    cache[dev].store(c, std::memory_order_relaxed);
+  }
+  return c;
+}
 
 // Records `msg` as the calling thread's murm_last_error() and returns `code`.
 int set_error(int code, const char* msg);

@@ -116,8 +116,8 @@ __device__ __forceinline__ bool sa_block(int BH, int nchunk, int& bh, int& chunk
 // ---------------------------------------------------------------------------
 // 16-bit tokens (bf16 / fp16): hi/lo split keys in LDS, 16x16x32 MFMA
 // ---------------------------------------------------------------------------
-template <typename T, int DP, bool WIDE>
-__global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p, int nchunk) {
+template <typename T, int DP, bool WIDE, int W = SA16_WAVES>
+__global__ __launch_bounds__(64 * W) void sa_kernel16(SAParams p, int nchunk) {
   using V = typename Mfma16<T>::vec;
   constexpr int G = SAShape<DP>::G;
   constexpr int KC = DP / 32;
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(64 * SA16_WAVES) void sa_kernel16(SAParams p, int n
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int quad = lane >> 4, col = lane & 15;
-  const int tok0 = chunk * SAShape<DP, SA16_WAVES>::TOK + wave * (G * 16);
+  const int tok0 = chunk * SAShape<DP, W>::TOK + wave * (G * 16);
 
   // WIDE (16-byte aligned rows, D % 8 == 0): the wave's token rows are
   // requested before the keys are staged, unconditionally from clamped rows
@@ -515,9 +515,9 @@ __global__ __launch_bounds__(256) void gather_out_kernel(OutParams p) {
 // table is staged in LDS (row stride table_stride) in turn and every thread keeps
 // the outputs of its GO_PASSES tokens in registers across the rounds.
 constexpr int GO_THREADS = 512;
-constexpr int GO_PASSES = 8;
+constexpr int GO_PASSES_MAX = 8;
 
-template <typename T, int DP, bool WIDE>
+template <typename T, int DP, bool WIDE, int GO_PASSES = GO_PASSES_MAX>
 __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p, int nchunk) {
   constexpr int DCH = DP / 8, TPP = GO_THREADS / DCH, RSD = table_stride<DP>();
   extern __shared__ __align__(16) unsigned char smem[];
@@ -587,20 +587,29 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
   const int Mp = (p.M + 15) & ~15;
   const int BH = p.B * p.H;
   if constexpr (sizeof(T) == 2) {
-    using S = SAShape<DP, SA16_WAVES>;
-    const int nchunk = (p.N + S::TOK - 1) / S::TOK;
-    const dim3 grid = sa_grid(BH, nchunk);
     const size_t lds = 2 * (size_t)Mp * (DP + 8) * sizeof(T);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     const bool wide = p.q.vec && p.D % 8 == 0;
-    const void* fn = wide ? reinterpret_cast<const void*>(&sa_kernel16<T, DP, true>)
-                          : reinterpret_cast<const void*>(&sa_kernel16<T, DP, false>);
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    auto go = [&](auto w_c) -> hipError_t {
+      constexpr int W = decltype(w_c)::value;
+      const int nchunk = (p.N + SAShape<DP, W>::TOK - 1) / SAShape<DP, W>::TOK;
+      const dim3 grid = sa_grid(BH, nchunk);
+      const void* fn = wide ? reinterpret_cast<const void*>(&sa_kernel16<T, DP, true, W>)
+                            : reinterpret_cast<const void*>(&sa_kernel16<T, DP, false, W>);
+      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+      if (wide)
+        MURM_LAUNCH((sa_kernel16<T, DP, true, W>), grid, dim3(64 * W), lds, st, p, nchunk);
+      else
+        MURM_LAUNCH((sa_kernel16<T, DP, false, W>), grid, dim3(64 * W), lds, st, p, nchunk);
+      return hipSuccess;
+    };
+    // half-size blocks (4 waves) when 8-wave blocks would leave CUs idle
+    using S8 = SAShape<DP, SA16_WAVES>;
+    const int blocks8 = (int)sa_grid(BH, (p.N + S8::TOK - 1) / S8::TOK).x;
+    hipError_t e = blocks8 >= device_cus() ? go(std::integral_constant<int, SA16_WAVES>{})
+                                           : go(std::integral_constant<int, SA16_WAVES / 2>{});
     if (e != hipSuccess) return e;
-    if (wide)
-      MURM_LAUNCH((sa_kernel16<T, DP, true>), grid, dim3(64 * SA16_WAVES), lds, st, p, nchunk);
-    else
-      MURM_LAUNCH((sa_kernel16<T, DP, false>), grid, dim3(64 * SA16_WAVES), lds, st, p, nchunk);
   } else {
     if (p.ksplit) return hipErrorInvalidValue;  // float32 tokens use the float32 keys
     const int nchunk = (p.N + SAShape<DP>::TOK - 1) / SAShape<DP>::TOK;
@@ -621,18 +630,26 @@ hipError_t launch_out_t(const OutParams& p, hipStream_t st) {
   if (lds <= 150 * 1024) {
     constexpr int TPP = GO_THREADS / (DP / 8);
     const int BH = p.B * p.H;
-    const int nchunk = (p.N + GO_PASSES * TPP - 1) / (GO_PASSES * TPP);
     const bool wide = (!p.base.p || p.base.vec) && p.D % 4 == 0;
-    const void* fn = wide ? reinterpret_cast<const void*>(&gather_out_lds_kernel<T, DP, true>)
-                          : reinterpret_cast<const void*>(&gather_out_lds_kernel<T, DP, false>);
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
-    if (wide)
-      MURM_LAUNCH((gather_out_lds_kernel<T, DP, true>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
-    else
-      MURM_LAUNCH((gather_out_lds_kernel<T, DP, false>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
-    return hipGetLastError();
+    auto go = [&](auto np_c) -> hipError_t {
+      constexpr int NP = decltype(np_c)::value;
+      const int nchunk = (p.N + NP * TPP - 1) / (NP * TPP);
+      const void* fn = wide ? reinterpret_cast<const void*>(&gather_out_lds_kernel<T, DP, true, NP>)
+                            : reinterpret_cast<const void*>(&gather_out_lds_kernel<T, DP, false, NP>);
+      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+      dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
+      if (wide)
+        MURM_LAUNCH((gather_out_lds_kernel<T, DP, true, NP>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
+      else
+        MURM_LAUNCH((gather_out_lds_kernel<T, DP, false, NP>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
+      return hipGetLastError();
+    };
+    // half the passes per block when full blocks would leave CUs idle
+    const int full = TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) *
+                     ((p.N + GO_PASSES_MAX * TPP - 1) / (GO_PASSES_MAX * TPP));
+    if (full >= device_cus()) return go(std::integral_constant<int, GO_PASSES_MAX>{});
+    return go(std::integral_constant<int, GO_PASSES_MAX / 2>{});
   }
   constexpr int TPB = 256 / (DP / 8);
   dim3 grid((p.N + TPB - 1) / TPB, p.B * p.H);

@@ -576,6 +576,12 @@ inline bool tables_fit(int nt, int M, int DP) {
   return (size_t)nt * M * rsd * 4 + (size_t)M * 4 <= 150 * 1024;
 }
 
+// a grid of blocks of `tokens` tokens per (b,h) fills every CU (otherwise the
+// launchers take blocks of fewer passes)
+inline bool tok_grid_fills(int BH, int N, int tokens) {
+  return TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * ((N + tokens - 1) / tokens) >= device_cus();
+}
+
 // unconditional token loads for every row the kernel reads (see raw8s)
 inline bool wide_rows(std::initializer_list<const TokView*> views, int D) {
   if (D % 4 != 0) return false;
@@ -618,7 +624,8 @@ hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
     // tokens per lane whose loads are all in flight at once: 8 (16-bit tokens,
     // two token rows) or 4 (float32 tokens or three token rows)
     if (p.dkv) return launch_tok_bwd_lds<T, DP, 4, true>(p, nt, st);
-    if (sizeof(T) == 2) return launch_tok_bwd_lds<T, DP, 8, false>(p, nt, st);
+    if (sizeof(T) == 2 && tok_grid_fills(p.B * p.H, p.N, 8 * TokShape<DP>::TPP))
+      return launch_tok_bwd_lds<T, DP, 8, false>(p, nt, st);
     return launch_tok_bwd_lds<T, DP, 4, false>(p, nt, st);
   }
   constexpr int TPB = 256 / (DP / 8);
@@ -664,7 +671,10 @@ hipError_t launch_tok_grad_t(const TokGradParams& p, hipStream_t st) {
   if (nt > 0 && tables_fit(1, p.M, DP)) {
     // registers: dq only (the slot-key gradient terms go to dq) keeps 8 passes
     // of tokens, with separate token-key / token-value gradients 4
-    if (p.shared_kv) return launch_tok_grad_lds<T, DP, 8, false>(p, nt, st);
+    if (p.shared_kv) {
+      if (tok_grid_fills(p.B * p.H, p.N, 8 * TokShape<DP>::TPP)) return launch_tok_grad_lds<T, DP, 8, false>(p, nt, st);
+      return launch_tok_grad_lds<T, DP, 4, false>(p, nt, st);
+    }
     return launch_tok_grad_lds<T, DP, 4, true>(p, nt, st);
   }
   constexpr int TPB = 256 / (DP / 8);
