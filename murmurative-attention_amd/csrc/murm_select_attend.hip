@@ -329,9 +329,10 @@ __global__ __launch_bounds__(64 * W) void sa_kernel16(SAParams p, int nchunk) {
 // ---------------------------------------------------------------------------
 // float32 tokens: f32 keys in LDS, 16x16x4 f32 MFMA, exact softmax scores
 // ---------------------------------------------------------------------------
-template <int DP>
+// G: 16-token groups per wave (fewer on small grids, so more CUs share the
+// float32 MFMA work)
+template <int DP, int G = SAShape<DP>::G>
 __global__ __launch_bounds__(256) void sa_kernel32(SAParams p, int nchunk) {
-  constexpr int G = SAShape<DP>::G;
   constexpr int KK = DP / 4;
   constexpr int ROW = DP + 4;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -377,7 +378,7 @@ __global__ __launch_bounds__(256) void sa_kernel32(SAParams p, int nchunk) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int quad = lane >> 4, col = lane & 15;
-  const int tok0 = chunk * SAShape<DP>::TOK + wave * (G * 16);
+  const int tok0 = chunk * (SAShape<DP>::WAVES * G * 16) + wave * (G * 16);
   if (tok0 >= p.N) return;
 
   float bq[G][KK];
@@ -612,14 +613,23 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
     if (e != hipSuccess) return e;
   } else {
     if (p.ksplit) return hipErrorInvalidValue;  // float32 tokens use the float32 keys
-    const int nchunk = (p.N + SAShape<DP>::TOK - 1) / SAShape<DP>::TOK;
-    const dim3 grid = sa_grid(BH, nchunk);
     const size_t lds = (size_t)Mp * (DP + 4) * sizeof(float);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sa_kernel32<DP>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    auto go = [&](auto g_c) -> hipError_t {
+      constexpr int G = decltype(g_c)::value;
+      constexpr int TOK = SAShape<DP>::WAVES * G * 16;
+      const int nchunk = (p.N + TOK - 1) / TOK;
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sa_kernel32<DP, G>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+      MURM_LAUNCH((sa_kernel32<DP, G>), sa_grid(BH, nchunk), dim3(256), lds, st, p, nchunk);
+      return hipSuccess;
+    };
+    // one token group per wave when full groups would leave CUs idle
+    const int full = (int)sa_grid(BH, (p.N + SAShape<DP>::TOK - 1) / SAShape<DP>::TOK).x;
+    hipError_t e = full >= device_cus() ? go(std::integral_constant<int, SAShape<DP>::G>{})
+                                        : go(std::integral_constant<int, 1>{});
     if (e != hipSuccess) return e;
-    MURM_LAUNCH((sa_kernel32<DP>), grid, dim3(256), lds, st, p, nchunk);
   }
   return hipGetLastError();
 }

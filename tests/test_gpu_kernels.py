@@ -60,6 +60,9 @@ SA_CASES = [
     (1, 2, 64, 32, 64, {"effective_M": 5}),
     (2, 2, 48, 32, 64, {"mask": True}),
     (1, 2, 48, 32, 64, {"bias": True}),
+    # a grid that fills the device: full-size select blocks (the small cases
+    # above take the half-size blocks of small grids)
+    (1, 16, 4096, 64, 64, {}),
     (1, 2, 64, 64, 128, {"scale": 0.3}),
 ]
 
