@@ -851,6 +851,7 @@ static int murmurate_fwd_enqueue(int dtype, int slot_dtype, int B, int H, int N,
     if (last) break;
     SegParams s = seg_base(B, H, N, D, M);
     s.idx = L.idx[r]; s.wgt = L.w[r]; s.va = kv; s.vb = vv; s.b_same_as_a = shared;
+    s.uniq_idx = 1;  // the select kernel names 7 distinct slots per token
     s.sk_old = L.sk[r]; s.sv_old = L.sv[r]; s.sk_new = L.sk[r + 1]; s.sv_new = L.sv[r + 1];
     s.ksum = L.ksum[r]; s.vsum = shared ? nullptr : L.vsum[r]; s.wsum = L.wsum[r];
     s.alpha = (float)alpha; s.gamma = (float)gamma; s.diffuse = 1;
@@ -942,6 +943,7 @@ static int murmurate_bwd_enqueue(int dtype, int slot_dtype, int B, int H, int N,
     // EMA backward (carries ping-pong: the halo rows read the other buffer)
     SegParams s = seg_base(B, H, N, D, M);
     s.idx = L.idx[r]; s.wgt = wr(r); s.ds = G.ds[r]; s.ds_scale = c; s.va = qv; s.vb = gv;
+    s.uniq_idx = 1;  // the forward's select kernel named 7 distinct slots per token
     s.carry_k = last ? nullptr : G.ck[(r + 1) & 1];
     s.carry_v = last ? nullptr : G.cv[(r + 1) & 1];
     if (r > 0) {

@@ -82,6 +82,7 @@ struct SegParams {
   TokView va;            // UPDATE: token keys; ATTBWD: queries
   TokView vb;            // UPDATE: token values; ATTBWD: grad of the attend output
   int b_same_as_a;       // UPDATE: token values are the token keys
+  int uniq_idx;          // 1: every token's slots are distinct (indices from the select kernel)
   // UPDATE
   const float* sk_old; const float* sv_old;  // fp32 [BH, M, D]
   float* sk_new; float* sv_new;              // fp32 [BH, M, D] (null: sums only)

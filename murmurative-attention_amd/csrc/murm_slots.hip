@@ -700,13 +700,15 @@ void seg_mma_kernel(SegParams p, PartParams pp) {
       const uint32_t sl = sj - (uint32_t)s0;  // slots of this group; others wrap past MS
       if (sl >= (uint32_t)MS || sj >= (uint32_t)p.M) continue;
       uint32_t before = 0, after = 0;
+      if (!p.uniq_idx) {  // caller-given indices may repeat a slot
 #pragma unroll
-      for (int x = 0; x < KN; ++x) {
-        const uint32_t hit = idx_at(ir, x) == sj ? 1u : 0u;
-        before |= (x < j ? hit : 0u) << x;
-        after |= (x > j ? hit : 0u) << x;
+        for (int x = 0; x < KN; ++x) {
+          const uint32_t hit = idx_at(ir, x) == sj ? 1u : 0u;
+          before |= (x < j ? hit : 0u) << x;
+          after |= (x > j ? hit : 0u) << x;
+        }
+        if (before) continue;
       }
-      if (before) continue;
       float c[KINDS];
 #pragma unroll
       for (int kind = 0; kind < KINDS; ++kind) c[kind] = pc[kind][q];
