@@ -1044,47 +1044,60 @@ __global__ void to_state4_kernel(SlotConv<const T*, float*> c0, SlotConv<const T
   }
 }
 
-// The same conversion with the keys (blockIdx.y == 0) also written split for
-// the 16-bit select kernel: the keys' items run over every element of the
-// split table (Mp rows of DP dims, zero past M and D), the values' over the
-// tensor as to_state4_kernel does.
-template <typename T, typename TT>
-__global__ void to_state_split_kernel(SlotConv<const T*, float*> ck, SlotConv<const T*, float*> cv, TT* split,
-                                      int H, int M, int D, int DP, int total_k, int total_v) {
-  const int D4 = (D + 3) >> 2;
-  if (blockIdx.y == 1) {
-    for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < total_v; q += gridDim.x * blockDim.x) {
-      const int row = q / D4, d0 = (q - row * D4) * 4;
-      const int bh = row / M, m = row - bh * M, b = bh / H, h = bh - b * H;
-      const T* sp = cv.src + b * cv.sb + h * cv.sh + (int64_t)m * cv.sm + d0;
-      float* o = cv.dst + (int64_t)row * D + d0;
-      for (int e = 0; e < 4 && d0 + e < D; ++e) o[e] = to_f(sp[e]);
-    }
-    return;
-  }
-  const int Mp = ksplit_mp(M), srow = ksplit_row(DP), DP4 = DP / 4;
-  for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < total_k; q += gridDim.x * blockDim.x) {
-    const int row = q / DP4, d0 = (q - row * DP4) * 4;
-    const int bh = row / Mp, m = row - bh * Mp, b = bh / H, h = bh - b * H;
-    float f[4] = {0.f, 0.f, 0.f, 0.f};
-    if (m < M) {
-      const T* sp = ck.src + b * ck.sb + h * ck.sh + (int64_t)m * ck.sm + d0;
-      float* o = ck.dst + ((int64_t)bh * M + m) * D + d0;
-      for (int e = 0; e < 4 && d0 + e < D; ++e) {
-        f[e] = to_f(sp[e]);
-        o[e] = f[e];
-      }
-    }
-    TT hi[4], lo[4];
+// The same conversion with the keys (blockIdx.z == 0) also written split for
+// the 16-bit select kernel (Mp rows of DP dims per head, zero past M and D)
+// and the values (blockIdx.z == 1) as float32 only.  Block x covers RPB rows
+// of one (b,h); a thread converts 4 dims of a row, with one vector load when
+// the tensor's rows are 4-element aligned (`vec`).
+template <typename T>
+__device__ __forceinline__ void load4f(const T* p, float (&f)[4]) {
+  if constexpr (sizeof(T) == 2) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    const T* e = reinterpret_cast<const T*>(&u);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      hi[e] = (TT)f[e];
-      lo[e] = (TT)(f[e] - (float)hi[e]);
-    }
-    TT* head = split + (size_t)bh * ksplit_head_elems(M, DP);
-    *reinterpret_cast<uint2*>(head + (size_t)m * srow + d0) = *reinterpret_cast<const uint2*>(hi);
-    *reinterpret_cast<uint2*>(head + ((size_t)Mp + m) * srow + d0) = *reinterpret_cast<const uint2*>(lo);
+    for (int i = 0; i < 4; ++i) f[i] = to_f(e[i]);
+  } else {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
   }
+}
+
+template <typename T, typename TT, int DP>
+__global__ __launch_bounds__(256) void to_state_split_kernel(SlotConv<const T*, float*> ck,
+                                                             SlotConv<const T*, float*> cv, TT* split, int H, int M,
+                                                             int D, int nrb, int vec_k, int vec_v) {
+  constexpr int DP4 = DP / 4, RPB = 256 / DP4;
+  const int bh = blockIdx.x / nrb, rb = blockIdx.x - bh * nrb;
+  const int b = bh / H, h = bh - b * H;
+  const int m = rb * RPB + (int)threadIdx.x / DP4, d0 = ((int)threadIdx.x % DP4) * 4;
+  const bool keys = blockIdx.z == 0;
+  const SlotConv<const T*, float*>& c = keys ? ck : cv;
+  const int Mp = ksplit_mp(M);
+  if (m >= (keys ? Mp : M)) return;
+  float f[4] = {0.f, 0.f, 0.f, 0.f};
+  if (m < M && d0 < D) {
+    const T* sp = c.src + b * c.sb + h * c.sh + (int64_t)m * c.sm + d0;
+    float* o = c.dst + ((int64_t)bh * M + m) * D + d0;
+    if (keys ? vec_k : vec_v) {  // D % 4 == 0: o is 16-byte aligned too
+      load4f(sp, f);
+      *reinterpret_cast<float4*>(o) = make_float4(f[0], f[1], f[2], f[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (d0 + e < D) o[e] = f[e] = to_f(sp[e]);
+    }
+  }
+  if (!keys) return;
+  TT hi[4], lo[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hi[e] = (TT)f[e];
+    lo[e] = (TT)(f[e] - (float)hi[e]);
+  }
+  TT* head = split + (size_t)bh * ksplit_head_elems(M, DP);
+  constexpr int SROW = DP + 8;  // ksplit_row(DP)
+  *reinterpret_cast<uint2*>(head + (size_t)m * SROW + d0) = *reinterpret_cast<const uint2*>(hi);
+  *reinterpret_cast<uint2*>(head + ((size_t)Mp + m) * SROW + d0) = *reinterpret_cast<const uint2*>(lo);
 }
 
 template <typename T>
@@ -1353,15 +1366,27 @@ hipError_t launch_du(const DuParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <typename T>
+bool rows_vec4(const SlotConv<const T*, float*>& c, int D) {
+  return (D & 3) == 0 && c.sb % 4 == 0 && c.sh % 4 == 0 && c.sm % 4 == 0 &&
+         reinterpret_cast<uintptr_t>(c.src) % (4 * sizeof(T)) == 0;
+}
+
 template <typename T, typename TT>
 hipError_t launch_split_t(const SlotConv<const T*, float*>& a, const SlotConv<const T*, float*>& b, bool has_b,
                           const KeySplitOut& ks, int B, int H, int M, int D, hipStream_t st) {
-  const int64_t tk = (int64_t)B * H * ksplit_mp(M) * (ks.DP / 4);
-  const int64_t tv = has_b ? (int64_t)B * H * M * ((D + 3) / 4) : 0;
-  if (tk >= (int64_t(1) << 30) || tv >= (int64_t(1) << 30)) return hipErrorInvalidValue;
-  const dim3 grid(grid1d(tk > tv ? tk : tv), has_b ? 2 : 1);
-  MURM_LAUNCH((to_state_split_kernel<T, TT>), grid, dim3(256), 0, st, a, b, static_cast<TT*>(ks.p), H, M, D, ks.DP,
-              (int)tk, (int)tv);
+  const int64_t BH = (int64_t)B * H;
+  const int rpb = 256 / (ks.DP / 4), nrb = (ksplit_mp(M) + rpb - 1) / rpb;
+  if (BH * nrb >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(BH * nrb), 1, has_b ? 2 : 1);
+  const int vk = rows_vec4(a, D), vv = has_b && rows_vec4(b, D);
+  TT* sp = static_cast<TT*>(ks.p);
+  switch (ks.DP) {
+    case 32: MURM_LAUNCH((to_state_split_kernel<T, TT, 32>), grid, dim3(256), 0, st, a, b, sp, H, M, D, nrb, vk, vv); break;
+    case 64: MURM_LAUNCH((to_state_split_kernel<T, TT, 64>), grid, dim3(256), 0, st, a, b, sp, H, M, D, nrb, vk, vv); break;
+    case 128: MURM_LAUNCH((to_state_split_kernel<T, TT, 128>), grid, dim3(256), 0, st, a, b, sp, H, M, D, nrb, vk, vv); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
