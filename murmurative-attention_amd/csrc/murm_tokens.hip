@@ -672,7 +672,16 @@ hipError_t launch_tok_grad_t(const TokGradParams& p, hipStream_t st) {
     // registers: dq only (the slot-key gradient terms go to dq) keeps 8 passes
     // of tokens, with separate token-key / token-value gradients 4
     if (p.shared_kv) {
-      if (tok_grid_fills(p.B * p.H, p.N, 8 * TokShape<DP>::TPP)) return launch_tok_grad_lds<T, DP, 8, false>(p, nt, st);
+      if (tok_grid_fills(p.B * p.H, p.N, 8 * TokShape<DP>::TPP)) {
+        // Two blocks per CU when two one-table blocks fit its LDS (d <= 64:
+        // about 110 VGPRs at 4 passes): the tables are staged one at a time
+        // and one block's staging runs beside the other's passes.
+        if (DP <= 64 && 2 * (size_t)p.M * TokShape<DP>::RSD * 4 <= 160 * 1024) {
+          if (wide_rows({&p.g}, p.D)) return launch_tok_grad_lds_s<T, DP, 4, false, true, true>(p, nt, st);
+          return launch_tok_grad_lds_s<T, DP, 4, false, false, true>(p, nt, st);
+        }
+        return launch_tok_grad_lds<T, DP, 8, false>(p, nt, st);
+      }
       return launch_tok_grad_lds<T, DP, 4, false>(p, nt, st);
     }
     return launch_tok_grad_lds<T, DP, 4, true>(p, nt, st);

@@ -336,22 +336,18 @@ def test_config3_headline_bf16_forward_backward():
                  oracle_dtype=torch.float32)
 
 
-@pytest.mark.timeout(900)
-def test_config4_causal_d128_subset():
-    # full-size kernel run (B=1, H=16, N=65536, d=128, causal); the oracle
-    # replays heads 0 and 15 (heads are independent)
-    _case("config 4")
-    B, H, N, D, M, R = 1, 16, 65536, 128, 256, 3
+def check_heads(dtype, B, H, N, D, M, R, causal, heads):
+    """Full-size kernel run; the oracle replays the given heads (heads are
+    independent), plus size-independent properties over all heads."""
     q, sk, sv, go = seeded([(B, H, N, D), (B, H, M, D), (B, H, M, D), (B, H, N, D)], 42, [None, None, 0.02, None])
-    dtype = torch.bfloat16
     q, sk, sv, go = (t.to(dtype) for t in (q, sk, sv, go))
     out, idx, w, per_round, gq, gsk, gsv = run_readme(q.to(DEV), sk.to(DEV), sv.to(DEV), go.to(DEV), None, R,
-                                                     True)
-    for h in (0, 15):
+                                                     causal)
+    for h in heads:
         sl = slice(h, h + 1)
         forced = [p[:, sl].cpu() for p in per_round]
         o_out, o_w, trace, o_gq, o_gsk, o_gsv = oracle_readme(q[:, sl], sk[:, sl], sv[:, sl], go[:, sl], None, R,
-                                                              True, forced, dtype=torch.float32)
+                                                              causal, forced, dtype=torch.float32)
         for r in range(R):
             check_selection(f"head {h} round {r}", forced[r], trace[r][4])
         assert_close(f"head {h} out", out[:, sl], o_out, dtype)
@@ -363,3 +359,19 @@ def test_config4_causal_d128_subset():
     wc = w.float().cpu()
     assert torch.allclose(wc.sum(-1), torch.ones_like(wc.sum(-1)), atol=1e-5) and (wc >= 0).all()
     assert torch.isfinite(out.float()).all() and torch.isfinite(gq.float()).all()
+
+
+@pytest.mark.timeout(900)
+def test_config4_causal_d128_subset():
+    # full-size kernel run (B=1, H=16, N=65536, d=128, causal); heads 0 and 15 replayed
+    _case("config 4")
+    check_heads(torch.bfloat16, 1, 16, 65536, 128, 256, 3, True, (0, 15))
+
+
+@pytest.mark.timeout(900)
+def test_d32_grid_filling_subset():
+    # d = 32 at a size whose token-kernel grid fills the device (16 heads of
+    # 16 chunks of 1024 tokens): the gradient pass runs two one-table blocks
+    # per CU; heads 0 and 15 replayed
+    _case("d32 grid filling")
+    check_heads(torch.float16, 1, 16, 16384, 32, 256, 3, False, (0, 15))
