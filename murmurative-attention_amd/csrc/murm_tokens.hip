@@ -680,6 +680,12 @@ hipError_t launch_tok_grad_t(const TokGradParams& p, hipStream_t st) {
           if (wide_rows({&p.g}, p.D)) return launch_tok_grad_lds_s<T, DP, 4, false, true, true>(p, nt, st);
           return launch_tok_grad_lds_s<T, DP, 4, false, false, true>(p, nt, st);
         }
+        // one table at a time (tables that do not fit together): blocks of 16
+        // passes stage each table for twice the tokens, where such blocks fill the device
+        if (!tables_fit(nt, p.M, DP) && tok_grid_fills(p.B * p.H, p.N, 16 * TokShape<DP>::TPP)) {
+          if (wide_rows({&p.g}, p.D)) return launch_tok_grad_lds_s<T, DP, 16, false, true, true>(p, nt, st);
+          return launch_tok_grad_lds_s<T, DP, 16, false, false, true>(p, nt, st);
+        }
         return launch_tok_grad_lds<T, DP, 8, false>(p, nt, st);
       }
       return launch_tok_grad_lds<T, DP, 4, false>(p, nt, st);
