@@ -358,6 +358,124 @@ __global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams 
   }
 }
 
+// tok_bwd with the tables staged one at a time (they do not fit together)
+// for blocks of many passes: a table phase keeps one pass's token and index
+// rows in flight ahead, and every (token, j) partial dw lives in LDS beside
+// the table ([NP][TPP][7] floats), so a block stages each table once for NP
+// passes of tokens.  Tables g.sv then tk.dKk (the form without token-value
+// rows); dw is the sum of the two tables' dot products, as in the staged
+// kernel's one-table-at-a-time form.
+template <typename T, int DP, int NP, bool WIDE>
+__global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_seq_kernel(TokBwdParams p, int nchunk) {
+  using S = TokShape<DP>;
+  constexpr int DCH = S::DCH, TPP = S::TPP, RSD = S::RSD;
+  constexpr int JPL = (KN + DCH - 1) / DCH;  // weights finished per lane
+  extern __shared__ __align__(16) unsigned char smem[];
+  int bh, chunk;
+  if (!tok_block(p.B * p.H, nchunk, bh, chunk)) return;
+  const int b = bh / p.H, h = bh % p.H;
+  const int dc = threadIdx.x % DCH, sw = tok_swap<DP>();
+  const int tl = threadIdx.x / DCH;  // token of a pass
+  const int c_beg = chunk * NP * TPP;
+  float* tab = reinterpret_cast<float*>(smem);
+  float* tdw = tab + p.M * RSD;              // dW [M]
+  float* dwb = tdw + ((p.M + 3) & ~3);       // partial dw [NP][TPP][KN]
+  const int64_t tb = (int64_t)bh * p.M * p.D;
+  if (p.dW)
+    for (int i = threadIdx.x; i < p.M; i += blockDim.x) tdw[i] = p.dW[(int64_t)bh * p.M + i];
+  const int nph = (p.sv ? 1 : 0) + (p.dkk ? 1 : 0);
+  for (int ph = 0; ph < nph; ++ph) {
+    const bool is_sv = p.sv && ph == 0;
+    const TokView& tv = is_sv ? p.g : p.tk;
+    // index and token rows PF passes ahead: the first PF in flight while the
+    // table is staged, pass q + PF requested as pass q starts
+    constexpr int PF = NP < 8 ? NP : 8;
+    uint4 ix[NP];
+    Raw8<T> rx[NP];
+    auto fetch = [&](int q) {
+      const int n = min(c_beg + q * TPP + tl, p.N - 1);
+      ix[q] = *reinterpret_cast<const uint4*>(p.idx + ((int64_t)bh * p.N + n) * IDX_ROW);
+      rx[q] = raw8s<T, WIDE, DP>(tok_row<T>(tv, b, h, n), dc, sw, p.D);
+    };
+#pragma unroll
+    for (int q = 0; q < PF; ++q) fetch(q);
+    if (ph > 0) __syncthreads();  // the previous table is no longer read
+    stage_table<DP>(tab, (is_sv ? p.sv : p.dkk) + tb, p.M, p.D);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      if (q + PF < NP) fetch(q + PF);
+      const uint4 ir = ix[q];
+      float x[8];
+      unraw8s<T, DP>(rx[q], x, dc, sw, p.D);
+      // rows of slot j + 1 are read while slot j's are used
+      float v[2][8];
+      auto rows = [&](int j, int o) { lds8s<DP>(tab + idx_at(ir, j) * RSD, dc, sw, v[o]); };
+      rows(0, 0);
+      float* slot = dwb + (q * TPP + tl) * KN;
+#pragma unroll
+      for (int j = 0; j < KN; ++j) {
+        const int o = j & 1;
+        if (j + 1 < KN) rows(j + 1, o ^ 1);
+        float sacc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sacc += x[i] * v[o][i];
+        const float dw = group_sum<DCH>(sacc);
+        if (j % DCH == dc) slot[j] = ph == 0 ? dw : slot[j] + dw;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  __syncthreads();
+  // lane dc finishes weights j = dc, dc + DCH, ... of each pass; every
+  // pass's index row, weights and weight grads requested at once
+  uint4 fi[NP];
+  float fw[NP][JPL], fg[NP][JPL];
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    const int n = min(c_beg + q * TPP + tl, p.N - 1);
+    const int64_t row = (int64_t)bh * p.N + n;
+    fi[q] = *reinterpret_cast<const uint4*>(p.idx + row * IDX_ROW);
+#pragma unroll
+    for (int u = 0; u < JPL; ++u) {
+      const int j = dc + u * DCH;
+      fw[q][u] = j < KN ? p.w[row * KN + j] : 0.f;
+      fg[q][u] = (p.gw && j < KN) ? p.gw[row * KN + j] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    const uint4 ir = fi[q];
+    const float* wq = fw[q];
+    const float* gq = fg[q];
+    const int n = c_beg + q * TPP + tl;
+    const float* slot = dwb + (q * TPP + tl) * KN;
+    float mine[JPL];
+    float part = 0.f;
+#pragma unroll
+    for (int u = 0; u < JPL; ++u) {
+      const int jj = dc + u * DCH;
+      float m = 0.f;
+      if (jj < KN) {
+        m = nph > 0 ? slot[jj] : 0.f;
+        if (p.dW) m += tdw[idx_at(ir, jj)];
+        m += gq[u];
+      }
+      mine[u] = m;
+      part += jj < KN ? wq[u] * m : 0.f;
+    }
+    const float dot = p.ds_out ? group_sum<DCH>(part) : 0.f;
+    const int64_t row = (int64_t)bh * p.N + n;
+#pragma unroll
+    for (int u = 0; u < JPL; ++u) {
+      const int jj = dc + u * DCH;
+      if (jj >= KN || n >= p.N) continue;
+      if (p.dw_out) p.dw_out[row * KN + jj] = mine[u];
+      if (p.ds_out) p.ds_out[row * KN + jj] = wq[u] * (mine[u] - dot);
+    }
+  }
+}
+
 // tok_grad with each round's tables staged in LDS in turn; a thread keeps the
 // gradients of its PASSES tokens in registers across the rounds.
 template <typename T, int DP, int PASSES, bool KV, bool WIDE, bool SEQ>
@@ -617,9 +735,35 @@ hipError_t launch_tok_bwd_lds(const TokBwdParams& p, int nt, hipStream_t st) {
   return launch_tok_bwd_lds_w<T, DP, NP, HV, false>(p, nt, st);
 }
 
+// LDS of tok_bwd_seq_kernel: one table, dW, the partial dw of NP passes
+template <int DP>
+size_t tok_bwd_seq_lds(int M, int np) {
+  return (size_t)M * TokShape<DP>::RSD * 4 + (size_t)((M + 3) & ~3) * 4 + (size_t)np * TokShape<DP>::TPP * KN * 4;
+}
+
+template <typename T, int DP, int NP, bool WIDE>
+hipError_t launch_tok_bwd_seq(const TokBwdParams& p, hipStream_t st) {
+  const int BH = p.B * p.H;
+  const int nchunk = (p.N + NP * TokShape<DP>::TPP - 1) / (NP * TokShape<DP>::TPP);
+  const size_t lds = tok_bwd_seq_lds<DP>(p.M, NP);
+  const void* fn = reinterpret_cast<const void*>(&tok_bwd_seq_kernel<T, DP, NP, WIDE>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
+  MURM_LAUNCH((tok_bwd_seq_kernel<T, DP, NP, WIDE>), grid, dim3(TOKS_THREADS), lds, st, p, nchunk);
+  return hipGetLastError();
+}
+
 template <typename T, int DP>
 hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
   const int nt = (p.sv ? 1 : 0) + (p.dkk ? 1 : 0) + (p.dkv ? 1 : 0);
+  // tables staged one at a time anyway: blocks of 16 passes keep their partial
+  // dw in LDS and stage each table once for twice the tokens of 8 passes
+  if (nt > 0 && !p.dkv && tables_fit(1, p.M, DP) && !tables_fit(nt, p.M, DP) &&
+      tok_bwd_seq_lds<DP>(p.M, 16) <= 160 * 1024 && tok_grid_fills(p.B * p.H, p.N, 16 * TokShape<DP>::TPP)) {
+    if (wide_rows({&p.g, &p.tk}, p.D)) return launch_tok_bwd_seq<T, DP, 16, true>(p, st);
+    return launch_tok_bwd_seq<T, DP, 16, false>(p, st);
+  }
   if (nt > 0 && tables_fit(1, p.M, DP)) {
     // tokens per lane whose loads are all in flight at once: 8 (16-bit tokens,
     // two token rows) or 4 (float32 tokens or three token rows)
