@@ -580,6 +580,80 @@ __global__ __launch_bounds__(GO_THREADS) void gather_out_lds_kernel(OutParams p,
   }
 }
 
+// gather_out for large grids: blocks of GO_PASSES_BIG passes, so each
+// round's table is staged once for twice the tokens of the standard block.
+// The outputs of all passes stay in registers across the rounds, so a
+// round's index rows and weights are requested PF passes ahead instead of
+// all at once (those of the first PF passes while the table is staged).
+constexpr int GO_PASSES_BIG = 16;
+
+template <typename T, int DP, bool WIDE>
+__global__ __launch_bounds__(GO_THREADS) void gather_out_big_kernel(OutParams p, int nchunk) {
+  constexpr int NP = GO_PASSES_BIG, PF = 2;
+  constexpr int DCH = DP / 8, TPP = GO_THREADS / DCH, RSD = table_stride<DP>();
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* tab = reinterpret_cast<float*>(smem);
+  int bh, chunk;
+  if (!tok_block(p.B * p.H, nchunk, bh, chunk)) return;
+  const int b = bh / p.H, h = bh % p.H;
+  const int dc = threadIdx.x % DCH, sw = tok_swap<DP>();
+  const int tl = threadIdx.x / DCH;
+  const int c_beg = chunk * NP * TPP;
+  float acc[NP][8];
+  if (p.base.p) {
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {  // residual rows in two halves of NP / 2 passes in flight
+      Raw8<T> rb[NP / 2];
+#pragma unroll
+      for (int q = 0; q < NP / 2; ++q)
+        rb[q] = raw8s<T, WIDE, DP>(tok_row<T>(p.base, b, h, min(c_beg + (h2 * NP / 2 + q) * TPP + tl, p.N - 1)),
+                                   dc, sw, p.D);
+#pragma unroll
+      for (int q = 0; q < NP / 2; ++q)
+        unraw8s<T, DP>(rb[q], acc[h2 * NP / 2 + q], dc, sw, p.D, c_beg + (h2 * NP / 2 + q) * TPP + tl < p.N);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < NP; ++q)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[q][i] = 0.f;
+  }
+  for (int r = 0; r < p.R; ++r) {
+    uint4 ix[NP];
+    float wv[NP][KN];
+    auto fetch = [&](int q) {
+      const int n = min(c_beg + q * TPP + tl, p.N - 1);
+      const int64_t row = (int64_t)bh * p.N + n;
+      ix[q] = *reinterpret_cast<const uint4*>(p.rp.idx[r] + row * IDX_ROW);
+      load_row7(p.rp.w[r] + row * KN, wv[q]);
+    };
+#pragma unroll
+    for (int q = 0; q < PF; ++q) fetch(q);
+    if (r > 0) __syncthreads();  // the previous round's table is no longer read
+    stage_table<DP>(tab, p.rp.a[r] + (int64_t)bh * p.M * p.D, p.M, p.D);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      if (q + PF < NP) fetch(q + PF);
+      const uint4 ir = ix[q];
+      const uint32_t sl[KN] = {ir.x & 0xFFFF, ir.x >> 16, ir.y & 0xFFFF, ir.y >> 16,
+                               ir.z & 0xFFFF, ir.z >> 16, ir.w & 0xFFFF};
+#pragma unroll
+      for (int j = 0; j < KN; ++j) {
+        float v[8];
+        lds8s<DP>(tab + sl[j] * RSD, dc, sw, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[q][i] += wv[q][j] * v[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    const int n = c_beg + q * TPP + tl;
+    if (n < p.N) store8s<T, DP>(tok_row_mut<T>(p.out, b, h, n), dc, sw, p.D, p.out.vec, acc[q]);
+  }
+}
+
 // 1-D grid of sa_block (tok_block ids)
 inline dim3 sa_grid(int BH, int nchunk) { return dim3(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk); }
 
@@ -655,6 +729,22 @@ hipError_t launch_out_t(const OutParams& p, hipStream_t st) {
         MURM_LAUNCH((gather_out_lds_kernel<T, DP, false, NP>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
       return hipGetLastError();
     };
+    // twice the passes where such blocks still fill the device
+    const int big = TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) *
+                    ((p.N + GO_PASSES_BIG * TPP - 1) / (GO_PASSES_BIG * TPP));
+    if (big >= device_cus()) {
+      const int nchunk = (p.N + GO_PASSES_BIG * TPP - 1) / (GO_PASSES_BIG * TPP);
+      const void* fn = wide ? reinterpret_cast<const void*>(&gather_out_big_kernel<T, DP, true>)
+                            : reinterpret_cast<const void*>(&gather_out_big_kernel<T, DP, false>);
+      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+      dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
+      if (wide)
+        MURM_LAUNCH((gather_out_big_kernel<T, DP, true>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
+      else
+        MURM_LAUNCH((gather_out_big_kernel<T, DP, false>), grid, dim3(GO_THREADS), lds, st, p, nchunk);
+      return hipGetLastError();
+    }
     // half the passes per block when full blocks would leave CUs idle
     const int full = TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) *
                      ((p.N + GO_PASSES_MAX * TPP - 1) / (GO_PASSES_MAX * TPP));
