@@ -757,9 +757,10 @@ hipError_t launch_tok_bwd_seq(const TokBwdParams& p, hipStream_t st) {
 template <typename T, int DP>
 hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
   const int nt = (p.sv ? 1 : 0) + (p.dkk ? 1 : 0) + (p.dkv ? 1 : 0);
-  // tables staged one at a time anyway: blocks of 16 passes keep their partial
-  // dw in LDS and stage each table once for twice the tokens of 8 passes
-  if (nt > 0 && !p.dkv && tables_fit(1, p.M, DP) && !tables_fit(nt, p.M, DP) &&
+  // tables of more than half the LDS (one block per CU in any form): blocks
+  // of 16 passes keep their partial dw in LDS and stage each table once for
+  // twice the tokens of 8 passes
+  if (nt > 0 && !p.dkv && tables_fit(1, p.M, DP) && (size_t)p.M * TokShape<DP>::RSD * 4 > 80 * 1024 &&
       tok_bwd_seq_lds<DP>(p.M, 16) <= 160 * 1024 && tok_grid_fills(p.B * p.H, p.N, 16 * TokShape<DP>::TPP)) {
     if (wide_rows({&p.g, &p.tk}, p.D)) return launch_tok_bwd_seq<T, DP, 16, true>(p, st);
     return launch_tok_bwd_seq<T, DP, 16, false>(p, st);
