@@ -375,3 +375,13 @@ def test_d32_grid_filling_subset():
     # per CU; heads 0 and 15 replayed
     _case("d32 grid filling")
     check_heads(torch.float16, 1, 16, 16384, 32, 256, 3, False, (0, 15))
+
+
+@pytest.mark.timeout(900)
+def test_fp32_m512_grid_filling_subset():
+    # float32 tokens, M = 512 (a slot table takes more than half the LDS) at
+    # a size whose 16-pass token blocks fill the device: the one-table-at-a-
+    # time backward kernels and the 16-pass output gather; heads 0 and 15
+    # replayed
+    _case("fp32 M=512 grid filling")
+    check_heads(torch.float32, 1, 16, 16384, 64, 512, 3, False, (0, 15))
