@@ -14,7 +14,8 @@
  *                   0 for slots shared over the batch).
  *   indices         int64 [B,H,N,7], weights float32 [B,H,N,7], contiguous.
  *   dtype codes     MURM_F32, MURM_F16, MURM_BF16.
- * Limits: 7 <= M <= 65535, 1 <= D <= 128, rounds <= 16, slots per token = 7.
+ * Limits: 7 <= M <= 65535, 1 <= D <= 128, rounds <= 16, slots per token = 7,
+ * N <= 2^24, B*H*N < 2^31 tokens, token row strides (sn) < 2^32 elements.
  * The entry points that select (murm_select_attend_fwd, murm_select_fwd,
  * murm_murmurate_fwd) also stage one head's slot keys in the 160 KiB LDS of
  * a CU, which bounds M by dtype and D: murm_select_max_m() returns the bound

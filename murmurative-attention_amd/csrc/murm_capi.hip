@@ -138,6 +138,8 @@ int check_geom(int dtype, int slot_dtype, int B, int H, int N, int D, int M) {
   if (D < 1 || D > 128) return fail(MURM_ERR_UNSUPPORTED, "head dim D=%d outside [1, 128]", D);
   if (M < KN || M > 65535) return fail(MURM_ERR_ARG, "M=%d outside [7, 65535] (7 slots are selected)", M);
   if (N > (1 << 24)) return fail(MURM_ERR_UNSUPPORTED, "N=%d too large", N);
+  if ((int64_t)B * H * N >= (int64_t(1) << 31))
+    return fail(MURM_ERR_UNSUPPORTED, "B*H*N=%lld tokens too many (at most 2^31 - 1)", (long long)B * H * N);
   return MURM_OK;
 }
 

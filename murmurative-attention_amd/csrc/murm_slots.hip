@@ -594,18 +594,25 @@ void seg_mma_kernel(SegParams p, PartParams pp) {
     u = rem % UPR;
     g4 = rem / UPR;
   };
+  // Addresses: the (b,h) bases are uniform; a token's row is one unsigned
+  // 32 x 32 -> 64-bit multiply-add on top (row numbers and strides < 2^32).
+  const T* va0 = tok_row<T>(p.va, b, h, 0);
+  const T* vb0 = tok_row<T>(p.vb, b, h, 0);
+  const uint32_t sna = (uint32_t)p.va.sn, snb = (uint32_t)p.vb.sn;
+  const uint32_t rbase = (uint32_t)bh * (uint32_t)p.N;
   auto fetch = [&](int n0) {
     // marking loads first, token rows last (nothing after them touches a register)
-    const int64_t row = (int64_t)bh * p.N + min(n0 + mt, p.N - 1);
-    pidx = *reinterpret_cast<const uint4*>(p.idx + row * IDX_ROW);
+    const uint32_t row = rbase + (uint32_t)min(n0 + mt, p.N - 1);
+    pidx = *reinterpret_cast<const uint4*>(p.idx + (uint64_t)row * IDX_ROW);
+    const uint64_t crow = (uint64_t)row * KN;
 #pragma unroll
     for (int q = 0; q < JPT; ++q) {
       const int j = min(JPT * mk + q, KN - 1);
       if (MODE == SEG_ATTBWD) {
-        pc[0][q] = p.ds[row * KN + j];  // scaled when marked
-        pc[KINDS - 1][q] = p.wgt[row * KN + j];
+        pc[0][q] = p.ds[crow + j];  // scaled when marked
+        pc[KINDS - 1][q] = p.wgt[crow + j];
       } else {
-        pc[0][q] = p.wgt[row * KN + j];
+        pc[0][q] = p.wgt[crow + j];
       }
     }
     if (wide) {
@@ -615,10 +622,11 @@ void seg_mma_kernel(SegParams p, PartParams pp) {
         if (GROUPS % MMA_THREADS != 0 && item >= GROUPS) continue;
         int v, u, g4;
         unit_of(item, v, u, g4);
-        const TokView& tv = v == 0 ? p.va : p.vb;
+        const T* base = (v == 0 ? va0 : vb0) + u * 8;
+        const uint32_t sn = v == 0 ? sna : snb;
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          px[g][k] = *reinterpret_cast<const uint4*>(tok_row<T>(tv, b, h, min(n0 + 4 * g4 + k, p.N - 1)) + u * 8);
+          px[g][k] = *reinterpret_cast<const uint4*>(base + (uint64_t)(uint32_t)min(n0 + 4 * g4 + k, p.N - 1) * sn);
       }
     }
   };
@@ -1288,6 +1296,8 @@ template <typename T, int DP>
 hipError_t launch_seg_t(const SegParams& p, int mode, const PartParams* pp, int stage, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     if (!pp || pp->nchunk <= 0 || pp->chunk_tokens % MSUBT != 0) return hipErrorInvalidValue;
+    // the MFMA kernels address token rows with 32-bit row numbers and strides
+    if ((uint64_t)p.va.sn >= (uint64_t(1) << 32) || (uint64_t)p.vb.sn >= (uint64_t(1) << 32)) return hipErrorInvalidValue;
     if (mode == SEG_ATTBWD) return launch_mma<T, DP, SEG_ATTBWD, 2, 1>(p, *pp, stage, st);
     // Update with one vector: blocks of two token groups over pairs of the
     // carved chunks (same waves per CU, half the partials to write and add).

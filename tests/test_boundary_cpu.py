@@ -136,3 +136,16 @@ def test_select_lds_bound_without_gpu():
                                     None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, fake, 0, 0, D, fake, 0, 0, D,
                                     None, 0, 0, 0, 0, fake, 0, 0, D, fake, fake, fake, 1 << 40, None)
         assert rc == capi.ERR_UNSUPPORTED and b"LDS" in lib.murm_last_error(), (dt, D)
+
+
+def test_token_count_bound_without_gpu():
+    # B*H*N of 2^31 tokens or more is refused on the host (the kernels number
+    # token rows with 32 bits), before any launch
+    lib = capi.load()
+    P = ctypes.c_void_p
+    fake = P(4096)
+    B, H, N, D, M = 1, 128, 1 << 24, 64, 256
+    rc = lib.murm_murmurate_fwd(capi.BF16, capi.BF16, B, H, N, D, M, 3, 0.9, 0.15, 0, 0, 0.0, fake, 0, 0, D,
+                                None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, fake, 0, 0, D, fake, 0, 0, D,
+                                None, 0, 0, 0, 0, fake, 0, 0, D, fake, fake, fake, 1 << 40, None)
+    assert rc == capi.ERR_UNSUPPORTED and b"tokens" in lib.murm_last_error()
