@@ -833,6 +833,12 @@ hipError_t launch_tok_grad_t(const TokGradParams& p, hipStream_t st) {
         }
         return launch_tok_grad_lds<T, DP, 8, false>(p, nt, st);
       }
+      // smaller grids: one-table blocks of 2 passes, two per CU, where they fill the device twice
+      if (DP <= 64 && 2 * (size_t)p.M * TokShape<DP>::RSD * 4 <= 160 * 1024 &&
+          tok_grid_fills(p.B * p.H, p.N, 4 * TokShape<DP>::TPP)) {
+        if (wide_rows({&p.g}, p.D)) return launch_tok_grad_lds_s<T, DP, 2, false, true, true>(p, nt, st);
+        return launch_tok_grad_lds_s<T, DP, 2, false, false, true>(p, nt, st);
+      }
       return launch_tok_grad_lds<T, DP, 4, false>(p, nt, st);
     }
     return launch_tok_grad_lds<T, DP, 4, true>(p, nt, st);
