@@ -523,6 +523,7 @@ int murm_select_attend_fwd(int dtype, int slot_dtype, int B, int H, int N, int D
   p.bias = bias; p.bs_sb = bs_sb; p.bs_sh = bs_sh; p.bs_sn = bs_sn; p.bs_sm = bs_sm;
   p.idx16 = L.idx; p.idx64 = indices; p.w = weights;
   p.ksplit = ksplit_out(dtype, L.ksp, D).p;
+  p.keys_hi_only = slot_dtype == dtype;  // keys exact in the token dtype: zero lo halves
   RUN(C_SA, "select_attend", launch_select_attend(dtype, DP, p, st));
   OutParams o{};
   o.base = none_tv();
@@ -555,6 +556,7 @@ int murm_select_fwd(int dtype, int slot_dtype, int B, int H, int N, int D, int M
   }
   SAParams p = sa_params(B, H, N, D, M, tv_of(q, q_sb, q_sh, q_sn, dtype), L.sk, effective_M, causal, 0.0);
   p.ksplit = ksplit_out(dtype, L.ksp, D).p;
+  p.keys_hi_only = slot_dtype == dtype;  // keys exact in the token dtype: zero lo halves
   p.mask = mask; p.mk_sb = mk_sb; p.mk_sh = mk_sh; p.mk_sn = mk_sn; p.mk_sm = mk_sm;
   p.bias = bias; p.bs_sb = bs_sb; p.bs_sh = bs_sh; p.bs_sn = bs_sn; p.bs_sm = bs_sm;
   p.idx16 = nullptr; p.idx64 = indices;
@@ -846,6 +848,7 @@ static int murmurate_fwd_enqueue(int dtype, int slot_dtype, int B, int H, int N,
     SAParams p = sa_params(B, H, N, D, M, qv, L.sk[r], effective_M, causal, scale);
     p.mask = mask; p.mk_sb = mk_sb; p.mk_sh = mk_sh; p.mk_sn = mk_sn; p.mk_sm = mk_sm;
     p.ksplit = ksplit_out(dtype, L.ksp[r], D).p;
+    p.keys_hi_only = r == 0 && slot_dtype == dtype;  // the caller's keys: zero lo halves
     p.idx16 = L.idx[r];
     p.idx64 = last ? indices_last : nullptr;
     p.w = last ? weights_last : L.w[r];

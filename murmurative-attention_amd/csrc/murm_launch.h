@@ -47,6 +47,7 @@ struct SAParams {
   // 16-bit tokens: the keys already split into hi / lo halves of the token
   // dtype in the kernel's LDS layout (KeySplit below); null: split from sk
   const void* ksplit;
+  int keys_hi_only;  // 1: the lo halves of ksplit are all zero (keys of the token dtype)
 };
 
 // Slot keys split for the 16-bit select kernel: per (b,h) a hi table then a lo

@@ -116,7 +116,10 @@ __device__ __forceinline__ bool sa_block(int BH, int nchunk, int& bh, int& chunk
 // ---------------------------------------------------------------------------
 // 16-bit tokens (bf16 / fp16): hi/lo split keys in LDS, 16x16x32 MFMA
 // ---------------------------------------------------------------------------
-template <typename T, int DP, bool WIDE, int W = SA16_WAVES>
+// HI: the keys are exact in the token dtype (lo halves all zero; the first
+// round of a call whose slot keys have the token dtype): only the hi halves
+// are copied and multiplied, which gives the same scores bit for bit.
+template <typename T, int DP, bool WIDE, int W = SA16_WAVES, bool HI = false>
 __global__ __launch_bounds__(64 * W) void sa_kernel16(SAParams p, int nchunk) {
   using V = typename Mfma16<T>::vec;
   constexpr int G = SAShape<DP>::G;
@@ -157,7 +160,8 @@ __global__ __launch_bounds__(64 * W) void sa_kernel16(SAParams p, int nchunk) {
   const int nq = p.ksplit ? 0 : Mp * (DP / 4);
   if (p.ksplit) {
     const size_t head = 2 * (size_t)Mp * ROW;
-    copy_to_lds(lhi, reinterpret_cast<const T*>(p.ksplit) + (size_t)bh * head, (int)(head * sizeof(T)));
+    copy_to_lds(lhi, reinterpret_cast<const T*>(p.ksplit) + (size_t)bh * head,
+                (int)((HI ? head / 2 : head) * sizeof(T)));
   }
   const bool vec4 = (p.D & 3) == 0;
   for (int i0 = threadIdx.x; i0 < nq; i0 += STB * blockDim.x) {
@@ -228,14 +232,15 @@ __global__ __launch_bounds__(64 * W) void sa_kernel16(SAParams p, int nchunk) {
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
       ahi[kc] = *reinterpret_cast<const V*>(lhi + arow * ROW + 32 * kc + 8 * quad);
-      alo[kc] = *reinterpret_cast<const V*>(llo + arow * ROW + 32 * kc + 8 * quad);
+      if constexpr (!HI) alo[kc] = *reinterpret_cast<const V*>(llo + arow * ROW + 32 * kc + 8 * quad);
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (!HI)
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc)
+      for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
-      for (int g = 0; g < G; ++g) acc[g] = mfma_16x16x32(alo[kc], bq[g][kc], acc[g]);
+        for (int g = 0; g < G; ++g) acc[g] = mfma_16x16x32(alo[kc], bq[g][kc], acc[g]);
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
@@ -309,7 +314,8 @@ __global__ __launch_bounds__(64 * W) void sa_kernel16(SAParams p, int nchunk) {
         for (int kc = 0; kc < KC; ++kc) {
           const int d0 = 32 * kc + 8 * quad;
           const V hv = *reinterpret_cast<const V*>(lhi + slot[j] * ROW + d0);
-          const V lv = *reinterpret_cast<const V*>(llo + slot[j] * ROW + d0);
+          V lv{};
+          if constexpr (!HI) lv = *reinterpret_cast<const V*>(llo + slot[j] * ROW + d0);
 #pragma unroll
           for (int i = 0; i < 8; ++i) part[j] += (float)bq[g][kc][i] * ((float)hv[i] + (float)lv[i]);
         }
@@ -669,15 +675,20 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
       constexpr int W = decltype(w_c)::value;
       const int nchunk = (p.N + SAShape<DP, W>::TOK - 1) / SAShape<DP, W>::TOK;
       const dim3 grid = sa_grid(BH, nchunk);
-      const void* fn = wide ? reinterpret_cast<const void*>(&sa_kernel16<T, DP, true, W>)
-                            : reinterpret_cast<const void*>(&sa_kernel16<T, DP, false, W>);
-      hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-      if (wide)
-        MURM_LAUNCH((sa_kernel16<T, DP, true, W>), grid, dim3(64 * W), lds, st, p, nchunk);
-      else
-        MURM_LAUNCH((sa_kernel16<T, DP, false, W>), grid, dim3(64 * W), lds, st, p, nchunk);
-      return hipSuccess;
+      auto run = [&](auto hi_c) -> hipError_t {
+        constexpr bool HI = decltype(hi_c)::value;
+        const void* fn = wide ? reinterpret_cast<const void*>(&sa_kernel16<T, DP, true, W, HI>)
+                              : reinterpret_cast<const void*>(&sa_kernel16<T, DP, false, W, HI>);
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        if (wide)
+          MURM_LAUNCH((sa_kernel16<T, DP, true, W, HI>), grid, dim3(64 * W), lds, st, p, nchunk);
+        else
+          MURM_LAUNCH((sa_kernel16<T, DP, false, W, HI>), grid, dim3(64 * W), lds, st, p, nchunk);
+        return hipSuccess;
+      };
+      if (p.ksplit && p.keys_hi_only) return run(std::true_type{});
+      return run(std::false_type{});
     };
     // half-size blocks (4 waves) when 8-wave blocks would leave CUs idle
     using S8 = SAShape<DP, SA16_WAVES>;
