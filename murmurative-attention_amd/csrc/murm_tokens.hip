@@ -165,16 +165,16 @@ __global__ __launch_bounds__(256) void tok_grad_kernel(TokGradParams p) {
 // ---------------------------------------------------------------------------
 constexpr int TOKS_THREADS = 512;
 
-template <int DP>
+template <int DP, int NT = TOKS_THREADS>
 struct TokShape {
   static constexpr int DCH = DP / 8;                   // lanes per token
-  static constexpr int TPP = TOKS_THREADS / DCH;       // tokens per pass
+  static constexpr int TPP = NT / DCH;                 // tokens per pass (NT threads)
   static constexpr int RSD = table_stride<DP>();       // staged row stride
 };
 
-template <typename T, int DP, int NP, bool HV, bool WIDE, bool SEQ>
-__global__ __launch_bounds__(TOKS_THREADS) void tok_bwd_lds_kernel(TokBwdParams p, int nchunk) {
-  using S = TokShape<DP>;
+template <typename T, int DP, int NP, bool HV, bool WIDE, bool SEQ, int NT = TOKS_THREADS>
+__global__ __launch_bounds__(NT) void tok_bwd_lds_kernel(TokBwdParams p, int nchunk) {
+  using S = TokShape<DP, NT>;
   constexpr int DCH = S::DCH, TPP = S::TPP, RSD = S::RSD;
   extern __shared__ __align__(16) unsigned char smem[];
   int bh, chunk;
@@ -754,6 +754,23 @@ hipError_t launch_tok_bwd_seq(const TokBwdParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Blocks of 1024 threads and 4 passes: the tokens and tables of an 8-pass
+// block of 512 threads, with 4 waves per SIMD instead of 2 to hide the LDS
+// and load latency (128 VGPRs; rows 16-byte aligned).
+template <typename T, int DP, bool WIDE>
+hipError_t launch_tok_bwd_1k(const TokBwdParams& p, int nt, hipStream_t st) {
+  using S = TokShape<DP, 1024>;
+  const int BH = p.B * p.H;
+  const int nchunk = (p.N + 4 * S::TPP - 1) / (4 * S::TPP);
+  const size_t lds = (size_t)nt * p.M * S::RSD * 4 + (size_t)p.M * 4;
+  const void* fn = reinterpret_cast<const void*>(&tok_bwd_lds_kernel<T, DP, 4, false, WIDE, false, 1024>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
+  MURM_LAUNCH((tok_bwd_lds_kernel<T, DP, 4, false, WIDE, false, 1024>), grid, dim3(1024), lds, st, p, nchunk);
+  return hipGetLastError();
+}
+
 template <typename T, int DP>
 hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
   const int nt = (p.sv ? 1 : 0) + (p.dkk ? 1 : 0) + (p.dkv ? 1 : 0);
@@ -769,8 +786,11 @@ hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
     // tokens per lane whose loads are all in flight at once: 8 (16-bit tokens,
     // two token rows) or 4 (float32 tokens or three token rows)
     if (p.dkv) return launch_tok_bwd_lds<T, DP, 4, true>(p, nt, st);
-    if (sizeof(T) == 2 && tok_grid_fills(p.B * p.H, p.N, 8 * TokShape<DP>::TPP))
+    if (sizeof(T) == 2 && tok_grid_fills(p.B * p.H, p.N, 8 * TokShape<DP>::TPP)) {
+      if (DP <= 64 && tables_fit(nt, p.M, DP) && wide_rows({&p.g, &p.tk, &p.tv}, p.D))
+        return launch_tok_bwd_1k<T, DP, true>(p, nt, st);
       return launch_tok_bwd_lds<T, DP, 8, false>(p, nt, st);
+    }
     return launch_tok_bwd_lds<T, DP, 4, false>(p, nt, st);
   }
   constexpr int TPB = 256 / (DP / 8);
