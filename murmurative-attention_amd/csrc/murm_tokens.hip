@@ -754,20 +754,20 @@ hipError_t launch_tok_bwd_seq(const TokBwdParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Blocks of 1024 threads and 4 passes: the tokens and tables of an 8-pass
-// block of 512 threads, with 4 waves per SIMD instead of 2 to hide the LDS
-// and load latency (128 VGPRs; rows 16-byte aligned).
-template <typename T, int DP, bool WIDE>
+// Blocks of 1024 threads and NP passes: the tokens and tables of a block of
+// 512 threads and 2 NP passes, with 4 waves per SIMD instead of 2 to hide the
+// LDS and load latency (at most 128 VGPRs; rows 16-byte aligned).
+template <typename T, int DP, bool WIDE, int NP = 4>
 hipError_t launch_tok_bwd_1k(const TokBwdParams& p, int nt, hipStream_t st) {
   using S = TokShape<DP, 1024>;
   const int BH = p.B * p.H;
-  const int nchunk = (p.N + 4 * S::TPP - 1) / (4 * S::TPP);
+  const int nchunk = (p.N + NP * S::TPP - 1) / (NP * S::TPP);
   const size_t lds = (size_t)nt * p.M * S::RSD * 4 + (size_t)p.M * 4;
-  const void* fn = reinterpret_cast<const void*>(&tok_bwd_lds_kernel<T, DP, 4, false, WIDE, false, 1024>);
+  const void* fn = reinterpret_cast<const void*>(&tok_bwd_lds_kernel<T, DP, NP, false, WIDE, false, 1024>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid(TOK_XCDS * ((BH + TOK_XCDS - 1) / TOK_XCDS) * nchunk);
-  MURM_LAUNCH((tok_bwd_lds_kernel<T, DP, 4, false, WIDE, false, 1024>), grid, dim3(1024), lds, st, p, nchunk);
+  MURM_LAUNCH((tok_bwd_lds_kernel<T, DP, NP, false, WIDE, false, 1024>), grid, dim3(1024), lds, st, p, nchunk);
   return hipGetLastError();
 }
 
@@ -791,6 +791,8 @@ hipError_t launch_tok_bwd_t(const TokBwdParams& p, hipStream_t st) {
         return launch_tok_bwd_1k<T, DP, true>(p, nt, st);
       return launch_tok_bwd_lds<T, DP, 8, false>(p, nt, st);
     }
+    if (sizeof(T) == 2 && DP <= 64 && tables_fit(nt, p.M, DP) && wide_rows({&p.g, &p.tk, &p.tv}, p.D))
+      return launch_tok_bwd_1k<T, DP, true, 2>(p, nt, st);
     return launch_tok_bwd_lds<T, DP, 4, false>(p, nt, st);
   }
   constexpr int TPB = 256 / (DP / 8);
