@@ -1334,9 +1334,10 @@ bool seg_two_stage(int dtype, int DP, int mode, const SegParams& p, const PartPa
 
 int seg_chunks(int B, int H, int N, int M, int D, int mode) {
   // token-chunk path, whole sub-chunks, at most NCMAX per (b,h): about 512
-  // (b,h,chunk,slot group) blocks for the update (two one-vector blocks fit a
-  // CU; a 16-bit update block holds 16384/d slots), about 256 (b,h,chunk)
-  // blocks for the attend backward (one two-vector block per CU by registers)
+  // (b,h,chunk,slot group) blocks for the update (a 16-bit update block holds
+  // 16384/d slots; with one vector the launcher pairs the chunks into blocks
+  // of two token groups), about 256 (b,h,chunk) for the attend backward (at
+  // d <= 64 two 128-slot groups per (b,h,chunk), two blocks per CU: 512)
   if (D > 128 || M < 1) return 0;
   const int BH = B * H;
   const int per = (N + SUB - 1) / SUB;
