@@ -837,7 +837,13 @@ static int murmurate_fwd_enqueue(int dtype, int slot_dtype, int B, int H, int N,
   const TokView qv = tv_of(q, q_sb, q_sh, q_sn, dtype);
   const TokView kv = shared ? qv : tv_of(tk, tk_sb, tk_sh, tk_sn, dtype);
   const TokView vv = shared ? qv : tv_of(tv, tv_sb, tv_sh, tv_sn, dtype);
-  {
+  // Slot tensors of the token dtype with 16-byte rows (and wide token rows):
+  // the first select reads them itself and writes the round's float32 state
+  // (no conversion launch); otherwise one conversion launch writes the state
+  // and the split keys.
+  const bool raw = slot_dtype == dtype && dtype != DT_F32 && D % 8 == 0 && qv.vec &&
+                   aligned16(sk, sk_sb, sk_sh, sk_sm, esize(dtype)) && aligned16(sv, sv_sb, sv_sh, sv_sm, esize(dtype));
+  if (!raw) {
     const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk[0]};
     const SlotConv<const void*, float*> cb{sv, sv_sb, sv_sh, sv_sm, L.sv[0]};
     const KeySplitOut ks = ksplit_out(dtype, L.ksp[0], D);
@@ -847,7 +853,13 @@ static int murmurate_fwd_enqueue(int dtype, int slot_dtype, int B, int H, int N,
     const bool last = r == rounds - 1;
     SAParams p = sa_params(B, H, N, D, M, qv, L.sk[r], effective_M, causal, scale);
     p.mask = mask; p.mk_sb = mk_sb; p.mk_sh = mk_sh; p.mk_sn = mk_sn; p.mk_sm = mk_sm;
-    p.ksplit = ksplit_out(dtype, L.ksp[r], D).p;
+    if (r == 0 && raw) {
+      p.raw_k = sk; p.rk_sb = sk_sb; p.rk_sh = sk_sh; p.rk_sm = sk_sm;
+      p.raw_v = sv; p.rv_sb = sv_sb; p.rv_sh = sv_sh; p.rv_sm = sv_sm;
+      p.st_k = L.sk[0]; p.st_v = L.sv[0];
+    } else {
+      p.ksplit = ksplit_out(dtype, L.ksp[r], D).p;
+    }
     p.keys_hi_only = r == 0 && slot_dtype == dtype;  // the caller's keys: zero lo halves
     p.idx16 = L.idx[r];
     p.idx64 = last ? indices_last : nullptr;

@@ -48,6 +48,17 @@ struct SAParams {
   // dtype in the kernel's LDS layout (KeySplit below); null: split from sk
   const void* ksplit;
   int keys_hi_only;  // 1: the lo halves of ksplit are all zero (keys of the token dtype)
+  // First round of a fused call whose slot tensors have the token dtype: the
+  // caller's keys and values (element strides over b, h, m; 16-byte aligned
+  // rows, D % 8 == 0) read by the kernel itself instead of a split table; the
+  // kernel writes the float32 state rows of both ([BH, M, D], each block of a
+  // head its share of the rows) for the kernels that follow.  raw_k null: unused.
+  const void* raw_k;
+  int64_t rk_sb, rk_sh, rk_sm;
+  const void* raw_v;
+  int64_t rv_sb, rv_sh, rv_sm;
+  float* st_k;
+  float* st_v;
 };
 
 // Slot keys split for the 16-bit select kernel: per (b,h) a hi table then a lo

@@ -106,6 +106,15 @@ __device__ __forceinline__ V load_operand8(const T* row, int d0, int D, bool vec
   return v;
 }
 
+// Eight 16-bit values (one 16-byte unit) widened to float32 and stored as two
+// float4 (dst 16-byte aligned).
+template <typename T>
+__device__ __forceinline__ void store8_f32(float* dst, const uint4& u) {
+  const T* e = reinterpret_cast<const T*>(&u);
+  reinterpret_cast<float4*>(dst)[0] = make_float4((float)e[0], (float)e[1], (float)e[2], (float)e[3]);
+  reinterpret_cast<float4*>(dst)[1] = make_float4((float)e[4], (float)e[5], (float)e[6], (float)e[7]);
+}
+
 // Blocks of the select kernels: (b,h) x token chunk as tok_block maps them
 // (with B*H a multiple of 8 all blocks of a head share one XCD's L2, where
 // the head's slot keys then arrive once).
@@ -119,8 +128,12 @@ __device__ __forceinline__ bool sa_block(int BH, int nchunk, int& bh, int& chunk
 // HI: the keys are exact in the token dtype (lo halves all zero; the first
 // round of a call whose slot keys have the token dtype): only the hi halves
 // are copied and multiplied, which gives the same scores bit for bit.
-template <typename T, int DP, bool WIDE, int W = SA16_WAVES, bool HI = false>
+// RAW (with HI): the hi table is read from the caller's key tensor (p.raw_k)
+// instead of a split table, and the block writes its share of the float32
+// state rows of the keys and values (p.st_k, p.st_v).
+template <typename T, int DP, bool WIDE, int W = SA16_WAVES, bool HI = false, bool RAW = false>
 __global__ __launch_bounds__(64 * W) void sa_kernel16(SAParams p, int nchunk) {
+  static_assert(!RAW || HI, "the caller's keys are the hi halves");
   using V = typename Mfma16<T>::vec;
   constexpr int G = SAShape<DP>::G;
   constexpr int KC = DP / 32;
@@ -157,8 +170,52 @@ __global__ __launch_bounds__(64 * W) void sa_kernel16(SAParams p, int nchunk) {
   // LDS, no registers); otherwise batches of STB float4 loads in flight per
   // thread, then the hi/lo split written as 8-byte LDS stores
   constexpr int STB = 8;
-  const int nq = p.ksplit ? 0 : Mp * (DP / 4);
-  if (p.ksplit) {
+  const int nq = (RAW || p.ksplit) ? 0 : Mp * (DP / 4);
+  if constexpr (RAW) {
+    // 16-byte units of the caller's key rows through registers into the
+    // padded LDS rows (zeros at d >= D and m >= M), one round of loads for
+    // the whole table at d <= 64; the rows [r0, r1) of this block's share
+    // also go to the float32 key state, and the same rows of the caller's
+    // values (one unit per thread in flight with the keys) to the value state
+    constexpr int UPR = DP / 8, RB = 32 / W;
+    const T* kb = static_cast<const T*>(p.raw_k) + b * p.rk_sb + h * p.rk_sh;
+    const T* vb = static_cast<const T*>(p.raw_v) + b * p.rv_sb + h * p.rv_sh;
+    float* stk = p.st_k + (size_t)bh * p.M * p.D;
+    float* stv = p.st_v + (size_t)bh * p.M * p.D;
+    const int rpc = (p.M + nchunk - 1) / nchunk;
+    const int r0 = chunk * rpc, r1 = min(p.M, r0 + rpc);
+    const int nu = Mp * UPR, nvu = max(0, r1 - r0) * UPR;
+    auto value_unit = [&](int i) {
+      const int d0 = (i % UPR) * 8;
+      return d0 < p.D ? *reinterpret_cast<const uint4*>(vb + (r0 + i / UPR) * p.rv_sm + d0) : make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto store_value = [&](int i, const uint4& u) {
+      const int d0 = (i % UPR) * 8;
+      if (d0 < p.D) store8_f32<T>(stv + (size_t)(r0 + i / UPR) * p.D + d0, u);
+    };
+    const int vi = threadIdx.x;
+    uint4 v0 = make_uint4(0u, 0u, 0u, 0u);
+    if (vi < nvu) v0 = value_unit(vi);
+    for (int i0 = threadIdx.x; i0 < nu; i0 += RB * blockDim.x) {
+      uint4 kk[RB];
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {
+        const int i = i0 + u * blockDim.x, m = i / UPR, d0 = (i % UPR) * 8;
+        kk[u] = make_uint4(0u, 0u, 0u, 0u);
+        if (i < nu && m < p.M && d0 < p.D) kk[u] = *reinterpret_cast<const uint4*>(kb + m * p.rk_sm + d0);
+      }
+#pragma unroll
+      for (int u = 0; u < RB; ++u) {
+        const int i = i0 + u * blockDim.x, m = i / UPR, d0 = (i % UPR) * 8;
+        if (i < nu) {
+          *reinterpret_cast<uint4*>(lhi + m * ROW + d0) = kk[u];
+          if (m >= r0 && m < r1 && d0 < p.D) store8_f32<T>(stk + (size_t)m * p.D + d0, kk[u]);
+        }
+      }
+    }
+    if (vi < nvu) store_value(vi, v0);
+    for (int i = vi + blockDim.x; i < nvu; i += blockDim.x) store_value(i, value_unit(i));  // few chunks per head
+  } else if (p.ksplit) {
     const size_t head = 2 * (size_t)Mp * ROW;
     copy_to_lds(lhi, reinterpret_cast<const T*>(p.ksplit) + (size_t)bh * head,
                 (int)((HI ? head / 2 : head) * sizeof(T)));
@@ -687,6 +744,14 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
           MURM_LAUNCH((sa_kernel16<T, DP, false, W, HI>), grid, dim3(64 * W), lds, st, p, nchunk);
         return hipSuccess;
       };
+      if (p.raw_k) {  // the caller's keys and values: wide rows only (checked by the caller too)
+        if (!wide || !p.raw_v || !p.st_k || !p.st_v || p.ksplit) return hipErrorInvalidValue;
+        const void* fn = reinterpret_cast<const void*>(&sa_kernel16<T, DP, true, W, true, true>);
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        MURM_LAUNCH((sa_kernel16<T, DP, true, W, true, true>), grid, dim3(64 * W), lds, st, p, nchunk);
+        return hipSuccess;
+      }
       if (p.ksplit && p.keys_hi_only) return run(std::true_type{});
       return run(std::false_type{});
     };
@@ -697,7 +762,7 @@ hipError_t launch_sa_t(const SAParams& p, hipStream_t st) {
                                            : go(std::integral_constant<int, SA16_WAVES / 2>{});
     if (e != hipSuccess) return e;
   } else {
-    if (p.ksplit) return hipErrorInvalidValue;  // float32 tokens use the float32 keys
+    if (p.ksplit || p.raw_k) return hipErrorInvalidValue;  // float32 tokens use the float32 keys
     const size_t lds = (size_t)Mp * (DP + 4) * sizeof(float);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     auto go = [&](auto g_c) -> hipError_t {
