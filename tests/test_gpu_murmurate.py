@@ -48,13 +48,26 @@ def oracle_readme(q, sk, sv, go, gw, rounds, causal, forced, alpha=0.9, gamma=0.
     return out, w, trace, q64.grad, sk64.grad, sv64.grad
 
 
+def _slot_rows(t, pad):
+    """t on the device; with pad > 0 as a view whose rows are pad elements
+    longer than D (a slice of a wider zero tensor)."""
+    if pad == 0:
+        return t.to(DEV)
+    wide = torch.zeros(*t.shape[:-1], t.shape[-1] + pad, dtype=t.dtype, device=DEV)
+    wide[..., :t.shape[-1]] = t.to(DEV)
+    return wide[..., :t.shape[-1]]
+
+
 def check_readme(dtype, B, H, N, D, M, rounds=3, causal=False, seed=42, sk_std=1.0, sv_std=0.02, with_gw=True,
-                 oracle_dtype=torch.float64, alpha=0.9, gamma=0.15):
+                 oracle_dtype=torch.float64, alpha=0.9, gamma=0.15, slot_dtype=None, slot_pad=0):
     q, sk, sv, go = seeded([(B, H, N, D), (B, H, M, D), (B, H, M, D), (B, H, N, D)], seed,
                            [None, sk_std, sv_std, None])
     gw = seeded([(B, H, N, 7)], seed + 1)[0] if with_gw else None
-    q, sk, sv, go = (t.to(dtype) for t in (q, sk, sv, go))
-    dq, dsk, dsv = (t.to(DEV) for t in (q, sk, sv))
+    sdt = slot_dtype or dtype
+    q, go = q.to(dtype), go.to(dtype)
+    sk, sv = sk.to(sdt), sv.to(sdt)
+    dq = q.to(DEV)
+    dsk, dsv = _slot_rows(sk, slot_pad), _slot_rows(sv, slot_pad)
     out, idx, w, per_round, gq, gsk, gsv = run_readme(dq, dsk, dsv, go.to(DEV),
                                                      gw.to(DEV) if gw is not None else None, rounds, causal,
                                                      alpha, gamma)
@@ -88,6 +101,25 @@ SMALL = [
     (torch.bfloat16, 1, 2, 160, 64, 520, 3, False),
     (torch.bfloat16, 1, 2, 2048, 128, 256, 3, True),
 ]
+
+
+# Slot tensors the first select reads itself (token dtype, 16-byte rows,
+# D % 8 == 0) and those that take the conversion launch (another dtype,
+# unaligned rows, D % 8 != 0): dtype, slot dtype, D, slot row padding
+SLOT_LAYOUTS = [
+    (torch.bfloat16, None, 40, 0),           # read by the select; LDS columns 40..63 zero
+    (torch.bfloat16, None, 64, 8),           # read by the select from rows of 72 elements
+    (torch.bfloat16, torch.float32, 64, 0),  # float32 slots: conversion
+    (torch.bfloat16, None, 64, 4),           # rows of 68 elements (136 bytes): conversion
+    (torch.float16, None, 36, 0),            # D % 8 != 0: conversion, non-vector token rows
+]
+
+
+@pytest.mark.parametrize("case", SLOT_LAYOUTS, ids=["d40", "pad8", "f32slots", "pad4", "d36"])
+def test_readme_slot_layouts(case):
+    dtype, sdt, D, pad = case
+    _case("slot layout", case)
+    check_readme(dtype, 1, 2, 300, D, 96, 3, False, slot_dtype=sdt, slot_pad=pad)
 
 
 @pytest.mark.parametrize("case", SMALL, ids=[f"s{i}" for i in range(len(SMALL))])
