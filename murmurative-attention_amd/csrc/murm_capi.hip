@@ -296,6 +296,24 @@ SAParams sa_params(int B, int H, int N, int D, int M, TokView q, const float* sk
   return p;
 }
 
+// Slot tensors of the token dtype (16-bit) with 16-byte rows and D % 8 == 0,
+// under wide token rows: the select kernel reads them itself and writes the
+// float32 state (no conversion launch); otherwise one conversion launch
+// writes the state and the split keys.
+bool slots_readable(int dtype, int slot_dtype, int D, const TokView& qv, const void* sk, int64_t sk_sb,
+                    int64_t sk_sh, int64_t sk_sm, const void* sv, int64_t sv_sb, int64_t sv_sh, int64_t sv_sm) {
+  return slot_dtype == dtype && dtype != DT_F32 && D % 8 == 0 && qv.vec &&
+         aligned16(sk, sk_sb, sk_sh, sk_sm, esize(dtype)) && aligned16(sv, sv_sb, sv_sh, sv_sm, esize(dtype));
+}
+void raw_slots(SAParams& p, const void* sk, int64_t sk_sb, int64_t sk_sh, int64_t sk_sm, const void* sv,
+               int64_t sv_sb, int64_t sv_sh, int64_t sv_sm, float* st_k, float* st_v) {
+  p.raw_k = sk; p.rk_sb = sk_sb; p.rk_sh = sk_sh; p.rk_sm = sk_sm;
+  p.raw_v = sv; p.rv_sb = sv_sb; p.rv_sh = sv_sh; p.rv_sm = sv_sm;
+  p.st_k = st_k; p.st_v = st_v;
+  p.ksplit = nullptr;
+  p.keys_hi_only = 1;
+}
+
 SegParams seg_base(int B, int H, int N, int D, int M) {
   SegParams p{};
   p.B = B; p.H = H; p.N = N; p.D = D; p.M = M; p.K = KN;
@@ -512,18 +530,24 @@ int murm_select_attend_fwd(int dtype, int slot_dtype, int B, int H, int N, int D
   if ((rc = need_ws(workspace, workspace_bytes, L.bytes))) return rc;
   const int DP = pick_dp(D);
   hipStream_t st = (hipStream_t)stream;
-  {
+  const TokView qv = tv_of(q, q_sb, q_sh, q_sn, dtype);
+  const bool raw = slots_readable(dtype, slot_dtype, D, qv, sk, sk_sb, sk_sh, sk_sm, sv, sv_sb, sv_sh, sv_sm);
+  if (!raw) {
     const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk};
     const SlotConv<const void*, float*> cb{sv, sv_sb, sv_sh, sv_sm, L.sv};
     const KeySplitOut ks = ksplit_out(dtype, L.ksp, D);
     RUN(C_CONV, "to_state", launch_to_state2(slot_dtype, ca, &cb, B, H, M, D, st, &ks));
   }
-  SAParams p = sa_params(B, H, N, D, M, tv_of(q, q_sb, q_sh, q_sn, dtype), L.sk, effective_M, causal, scale);
+  SAParams p = sa_params(B, H, N, D, M, qv, L.sk, effective_M, causal, scale);
   p.mask = mask; p.mk_sb = mk_sb; p.mk_sh = mk_sh; p.mk_sn = mk_sn; p.mk_sm = mk_sm;
   p.bias = bias; p.bs_sb = bs_sb; p.bs_sh = bs_sh; p.bs_sn = bs_sn; p.bs_sm = bs_sm;
   p.idx16 = L.idx; p.idx64 = indices; p.w = weights;
-  p.ksplit = ksplit_out(dtype, L.ksp, D).p;
-  p.keys_hi_only = slot_dtype == dtype;  // keys exact in the token dtype: zero lo halves
+  if (raw) {
+    raw_slots(p, sk, sk_sb, sk_sh, sk_sm, sv, sv_sb, sv_sh, sv_sm, L.sk, L.sv);
+  } else {
+    p.ksplit = ksplit_out(dtype, L.ksp, D).p;
+    p.keys_hi_only = slot_dtype == dtype;  // keys exact in the token dtype: zero lo halves
+  }
   RUN(C_SA, "select_attend", launch_select_attend(dtype, DP, p, st));
   OutParams o{};
   o.base = none_tv();
@@ -837,12 +861,7 @@ static int murmurate_fwd_enqueue(int dtype, int slot_dtype, int B, int H, int N,
   const TokView qv = tv_of(q, q_sb, q_sh, q_sn, dtype);
   const TokView kv = shared ? qv : tv_of(tk, tk_sb, tk_sh, tk_sn, dtype);
   const TokView vv = shared ? qv : tv_of(tv, tv_sb, tv_sh, tv_sn, dtype);
-  // Slot tensors of the token dtype with 16-byte rows (and wide token rows):
-  // the first select reads them itself and writes the round's float32 state
-  // (no conversion launch); otherwise one conversion launch writes the state
-  // and the split keys.
-  const bool raw = slot_dtype == dtype && dtype != DT_F32 && D % 8 == 0 && qv.vec &&
-                   aligned16(sk, sk_sb, sk_sh, sk_sm, esize(dtype)) && aligned16(sv, sv_sb, sv_sh, sv_sm, esize(dtype));
+  const bool raw = slots_readable(dtype, slot_dtype, D, qv, sk, sk_sb, sk_sh, sk_sm, sv, sv_sb, sv_sh, sv_sm);
   if (!raw) {
     const SlotConv<const void*, float*> ca{sk, sk_sb, sk_sh, sk_sm, L.sk[0]};
     const SlotConv<const void*, float*> cb{sv, sv_sb, sv_sh, sv_sm, L.sv[0]};
@@ -854,9 +873,7 @@ static int murmurate_fwd_enqueue(int dtype, int slot_dtype, int B, int H, int N,
     SAParams p = sa_params(B, H, N, D, M, qv, L.sk[r], effective_M, causal, scale);
     p.mask = mask; p.mk_sb = mk_sb; p.mk_sh = mk_sh; p.mk_sn = mk_sn; p.mk_sm = mk_sm;
     if (r == 0 && raw) {
-      p.raw_k = sk; p.rk_sb = sk_sb; p.rk_sh = sk_sh; p.rk_sm = sk_sm;
-      p.raw_v = sv; p.rv_sb = sv_sb; p.rv_sh = sv_sh; p.rv_sm = sv_sm;
-      p.st_k = L.sk[0]; p.st_v = L.sv[0];
+      raw_slots(p, sk, sk_sb, sk_sh, sk_sm, sv, sv_sb, sv_sh, sv_sm, L.sk[0], L.sv[0]);
     } else {
       p.ksplit = ksplit_out(dtype, L.ksp[r], D).p;
     }

@@ -67,12 +67,36 @@ SA_CASES = [
 ]
 
 
+def _slot_rows(t, pad):
+    """t on the device as a leaf; with pad > 0 a view whose rows are pad
+    elements longer than D (a slice of a wider zero tensor)."""
+    if pad == 0:
+        return t.to(DEV).requires_grad_(True)
+    wide = torch.zeros(*t.shape[:-1], t.shape[-1] + pad, dtype=t.dtype, device=DEV)
+    wide[..., :t.shape[-1]] = t.to(DEV)
+    leaf = wide.requires_grad_(True)
+    return leaf, leaf[..., :t.shape[-1]]
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "f16", "bf16"])
 @pytest.mark.parametrize("case", SA_CASES, ids=[f"c{i}" for i in range(len(SA_CASES))])
 def test_select_attend_op(dtype, case):
+    _check_select_attend(dtype, case)
+
+
+# bf16 tokens: 16-byte bf16 slot rows are read by the select kernel itself;
+# float32 slots and rows of 68 elements take the conversion launch
+@pytest.mark.parametrize("layout", [(None, 8), (torch.float32, 0), (None, 4)], ids=["pad8", "f32slots", "pad4"])
+def test_select_attend_op_slot_layouts(layout):
+    _check_select_attend(torch.bfloat16, (1, 2, 300, 64, 256, {}), *layout)
+
+
+def _check_select_attend(dtype, case, slot_dtype=None, slot_pad=0):
     B, H, N, D, M, fl = case
-    _print_case("select_attend", dtype, case)
+    _print_case("select_attend", dtype, case, slot_dtype, slot_pad)
     q, sk, sv, go, gw = _inputs(B, H, N, D, M, dtype)
+    if slot_dtype is not None:
+        sk, sv = sk.to(slot_dtype), sv.to(slot_dtype)
     mask = bias = None
     if fl.get("mask"):
         mask = torch.ones(B, 1, N, 1)
@@ -83,7 +107,11 @@ def test_select_attend_op(dtype, case):
     em = fl.get("effective_M", 0)
     scale = fl.get("scale")
     causal = fl.get("causal", False)
-    qd, skd, svd = (t.to(DEV).requires_grad_(True) for t in (q, sk, sv))
+    qd = q.to(DEV).requires_grad_(True)
+    if slot_pad:
+        (skl, skd), (svl, svd) = _slot_rows(sk, slot_pad), _slot_rows(sv, slot_pad)
+    else:
+        skd, svd = _slot_rows(sk, 0), _slot_rows(sv, 0)
     out, w, idx = MA.slot_select_attend(qd, skd, svd, mask=None if mask is None else mask.to(DEV),
                                         causal=causal, position_bias=None if bias is None else bias.to(DEV),
                                         scale=scale, effective_M=em)
@@ -100,8 +128,9 @@ def test_select_attend_op(dtype, case):
     assert_close("weights", w, o_w, dtype)
     ((o_out * go.double()).sum() + (o_w * gw.double()).sum()).backward()
     assert_close("grad_q", qd.grad, q64.grad, dtype)
-    assert_close("grad_slot_keys", skd.grad, sk64.grad, dtype)
-    assert_close("grad_slot_values", svd.grad, sv64.grad, dtype)
+    gsk, gsv = (skl.grad[..., :D], svl.grad[..., :D]) if slot_pad else (skd.grad, svd.grad)
+    assert_close("grad_slot_keys", gsk, sk64.grad, dtype)
+    assert_close("grad_slot_values", gsv, sv64.grad, dtype)
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "f16", "bf16"])
