@@ -174,7 +174,7 @@ __global__ __launch_bounds__(64 * W) void sa_kernel16(SAParams p, int nchunk) {
   if constexpr (RAW) {
     // 16-byte units of the caller's key rows through registers into the
     // padded LDS rows (zeros at d >= D and m >= M), one round of loads for
-    // the whole table at d <= 64; the rows [r0, r1) of this block's share
+    // tables of up to 2048 units (M = 256 at d = 64); the rows [r0, r1) of this block's share
     // also go to the float32 key state, and the same rows of the caller's
     // values (one unit per thread in flight with the keys) to the value state
     constexpr int UPR = DP / 8, RB = 32 / W;
