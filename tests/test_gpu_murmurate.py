@@ -106,20 +106,23 @@ SMALL = [
 # Slot tensors the first select reads itself (token dtype, 16-byte rows,
 # D % 8 == 0) and those that take the conversion launch (another dtype,
 # unaligned rows, D % 8 != 0): dtype, slot dtype, D, slot row padding
+# (N, M = 300, 96 unless given)
 SLOT_LAYOUTS = [
     (torch.bfloat16, None, 40, 0),           # read by the select; LDS columns 40..63 zero
     (torch.bfloat16, None, 64, 8),           # read by the select from rows of 72 elements
     (torch.bfloat16, torch.float32, 64, 0),  # float32 slots: conversion
     (torch.bfloat16, None, 64, 4),           # rows of 68 elements (136 bytes): conversion
     (torch.float16, None, 36, 0),            # D % 8 != 0: conversion, non-vector token rows
+    (torch.bfloat16, None, 64, 0, 2100, 7),  # more select blocks per head than slot rows
 ]
 
 
-@pytest.mark.parametrize("case", SLOT_LAYOUTS, ids=["d40", "pad8", "f32slots", "pad4", "d36"])
+@pytest.mark.parametrize("case", SLOT_LAYOUTS, ids=["d40", "pad8", "f32slots", "pad4", "d36", "m7"])
 def test_readme_slot_layouts(case):
-    dtype, sdt, D, pad = case
+    dtype, sdt, D, pad = case[:4]
+    N, M = case[4:] if len(case) > 4 else (300, 96)
     _case("slot layout", case)
-    check_readme(dtype, 1, 2, 300, D, 96, 3, False, slot_dtype=sdt, slot_pad=pad)
+    check_readme(dtype, 1, 2, N, D, M, 3, False, slot_dtype=sdt, slot_pad=pad)
 
 
 @pytest.mark.parametrize("case", SMALL, ids=[f"s{i}" for i in range(len(SMALL))])
