@@ -264,12 +264,18 @@ constexpr int CW = 8;       // coefficient row (7 used)
 constexpr int NCMAX = 32;   // chunks per (b,h)
 constexpr int NCB = 16;     // chunk partials loaded together by the reduction
 // reduction threads: with many chunks every (vector, row, 4 dims) item of a
-// group gets its own thread (up to 1024), so all chunk loads are in flight at
-// once; with few chunks (many heads) 256-thread blocks keep more groups resident
+// group (and, in the update, every row's weight sum) gets its own thread (up
+// to 1024), so all chunk loads are in flight at once; with few chunks (many
+// heads) 256-thread blocks keep more groups resident.  At 4 waves per SIMD
+// (128 VGPRs) a CU holds one block sized for two vectors (9 waves at
+// d = 64); on grids of more blocks than CUs the one-vector update takes
+// threads for its own items (5 waves), so three blocks share a CU (with one
+// block per CU the larger block's shorter epilogue loops win).
 constexpr int RED_THREADS = 1024;
-inline int red_threads(int nchunk, int DP) {
+inline int red_threads(int nchunk, int DP, int mode, const SegParams& p, int blocks) {
   if (nchunk < 8) return 256;
-  const int items = 2 * NSMAX * (DP / 4);
+  const int nv = (mode == SEG_UPDATE && p.b_same_as_a && blocks > device_cus()) ? 1 : 2;
+  const int items = nv * NSMAX * (DP / 4) + (mode == SEG_UPDATE ? NSMAX : 0);
   const int t = (items + 63) & ~63;
   return t > RED_THREADS ? RED_THREADS : t;
 }
@@ -1241,8 +1247,8 @@ hipError_t launch_part(const SegParams& p, const PartParams& pp, int nvec, int M
     MURM_LAUNCH((seg_partial_kernel<T, DP, MODE>), grid, dim3(threads), lds, st, p, pp);
   } else {
     const int G = (p.M + GS - 1) / GS;
-    MURM_LAUNCH((seg_reduce_kernel<DP, MODE>), dim3(XCDS * ((BH + XCDS - 1) / XCDS) * G),
-                       dim3(red_threads(pp.nchunk, DP)), 0,
+    const int blocks = XCDS * ((BH + XCDS - 1) / XCDS) * G;
+    MURM_LAUNCH((seg_reduce_kernel<DP, MODE>), dim3(blocks), dim3(red_threads(pp.nchunk, DP, MODE, p, blocks)), 0,
                        st, p, pp);
   }
   return hipGetLastError();
@@ -1271,9 +1277,11 @@ hipError_t launch_reduce(int mode, const SegParams& p, const PartParams& pp, hip
   const int G = (p.M + GS - 1) / GS;
   const dim3 grid(XCDS * ((BH + XCDS - 1) / XCDS) * G);
   if (mode == SEG_ATTBWD)
-    MURM_LAUNCH((seg_reduce_kernel<DP, SEG_ATTBWD>), grid, dim3(red_threads(pp.nchunk, DP)), 0, st, p, pp);
+    MURM_LAUNCH((seg_reduce_kernel<DP, SEG_ATTBWD>), grid, dim3(red_threads(pp.nchunk, DP, SEG_ATTBWD, p, grid.x)), 0,
+                st, p, pp);
   else
-    MURM_LAUNCH((seg_reduce_kernel<DP, SEG_UPDATE>), grid, dim3(red_threads(pp.nchunk, DP)), 0, st, p, pp);
+    MURM_LAUNCH((seg_reduce_kernel<DP, SEG_UPDATE>), grid, dim3(red_threads(pp.nchunk, DP, SEG_UPDATE, p, grid.x)), 0,
+                st, p, pp);
   return hipGetLastError();
 }
 
