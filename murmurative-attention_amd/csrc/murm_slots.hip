@@ -276,7 +276,10 @@ inline int red_threads(int nchunk, int DP, int mode, const SegParams& p, int blo
   if (nchunk < 8) return 256;
   const int nv = (mode == SEG_UPDATE && p.b_same_as_a && blocks > device_cus()) ? 1 : 2;
   const int items = nv * NSMAX * (DP / 4) + (mode == SEG_UPDATE ? NSMAX : 0);
-  const int t = (items + 63) & ~63;
+  int t = (items + 63) & ~63;
+  // two-vector blocks on such grids: 512 threads, two blocks per CU (a few
+  // threads take a second item)
+  if (nv == 2 && blocks > device_cus() && t > 512) t = 512;
   return t > RED_THREADS ? RED_THREADS : t;
 }
 
