@@ -203,7 +203,10 @@ int murm_slot_update_diffuse_fwd(int dtype, int slot_dtype, int B, int H, int N,
  *   q        selection queries (all rounds)
  *   x        residual base (NULL: q, the README form)
  *   tk, tv   update sources (NULL: q)
- *   sk, sv   initial slots (slot_dtype views, sb may be 0)
+ *   sk, sv   initial slots (slot_dtype views, sb may be 0); slots of the
+ *            token dtype (16-bit) with D % 8 == 0 and 16-byte aligned rows
+ *            and strides are read by the first select kernel itself, any
+ *            other slot dtype or layout takes one conversion launch more
  *   mask     optional [B,H,N,M] keep-mask view
  * Outputs: out = x + sum_r attend_r (through its strides), and for the last
  * round the int64 indices (may be NULL) and float32 weights.  `workspace`
